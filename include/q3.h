@@ -1,0 +1,142 @@
+/*
+ * q3.h -- C ABI of the gfx950 Qwen3 greedy-decode kernels (libq3.so).
+ *
+ * Every launcher takes device pointers, sizes and the hipStream_t to enqueue
+ * on; none allocates, synchronises or reads device memory from the host, so
+ * each can be recorded by hipStreamBeginCapture.  Each returns 0 on success or
+ * a hipError_t code (hipErrorInvalidValue for arguments that fail the
+ * launcher's own checks); q3_error_string() names a code.  BF16 tensors are
+ * raw uint16_t bits, row-major, contiguous unless a leading dimension is given.
+ *
+ * Reference interfaces replaced (file:line in alvinyuwen/starter):
+ *   rms_norm            engine/kernels/rmsnorm.py:48   engine/engine.py:75
+ *   add_norm            engine/kernels/fused.py:147    engine/engine.py:452
+ *   norm_rope           engine/kernels/fused.py:222    engine/engine.py:458
+ *   kv_to_cache         engine/kernels/fused.py:620    engine/engine.py:709-718
+ *   skinny_linear{,_t,_split}  fused.py:365,441,525    engine/engine.py:431 (_linear)
+ *   swiglu              engine/kernels/fused.py:872    engine/engine.py:464
+ *   decode_attention{,_gqa,_split}  fused.py:849,712,826  engine/engine.py:720-732
+ *   F.embedding / argmax / CUDA graph  engine/engine.py:768,812,833,1029-1065
+ */
+#ifndef Q3_H
+#define Q3_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- x_mode: how the GEMV's input rows are formed -------------------------- */
+#define Q3_X_PLAIN 0      /* x as given                                          */
+#define Q3_X_NORM 1       /* x = RMSNorm(x, norm_w) computed in the prologue      */
+#define Q3_X_EMBED_NORM 2 /* x = RMSNorm(embed[ids], norm_w); embed rows -> resid */
+
+/* ---- epi: what the projection does with its FP32 sums ---------------------- */
+#define Q3_EPI_STORE 0        /* y = bf16(acc)                                   */
+#define Q3_EPI_RESID 1        /* y = bf16(y + bf16(acc)), y is the residual      */
+#define Q3_EPI_SWIGLU 2       /* rows (gate_j, up_j) interleaved: y[j] = bf16(bf16(silu(g))*u) */
+#define Q3_EPI_ARGMAX 3       /* per-workgroup (max bf16 logit, lowest index)    */
+#define Q3_EPI_STORE_ARGMAX 4 /* both of the above                               */
+
+#define Q3_GEMV_MAX_M 8
+#define Q3_GEMV_MAX_NORM_K 4096
+
+const char *q3_error_string(int code);
+
+/* Decode projection for M <= 8 rows: y = epi(x' . W^T), x' per x_mode.
+ * Replaces _linear (engine.py:431) fused with the input norm (engine.py:790,
+ * fused.py:115 add_norm) and the residual / SwiGLU / argmax that follow it.
+ * W is [N, K]; K % 8 == 0; x, W 16-byte aligned; ldx % 8 == 0.
+ * EPI_SWIGLU writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
+ * [q3_gemv_partials(M, N, K), M]; finish with q3_argmax_finish. */
+int q3_gemv(int x_mode, const uint16_t *x, int ldx, const int64_t *ids,
+            const uint16_t *norm_w, float eps, uint16_t *resid_out,
+            const uint16_t *w, int M, int N, int K,
+            int epi, uint16_t *y, int ldy, float *part_val, int *part_idx,
+            hipStream_t stream);
+int q3_gemv_partials(int M, int N, int K);
+
+/* Dense projection for any M (MFMA, LDS-tiled): y = epi(x . W^T), epi in
+ * {STORE, RESID, SWIGLU}.  Replaces F.linear / cuBLAS in prefill and at decode
+ * batches above 8 (engine.py:439,450,803).  K % 64 == 0; x, W 16-byte aligned. */
+int q3_gemm(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
+            int epi, uint16_t *y, int ldy, hipStream_t stream);
+
+/* Row RMSNorm: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).  rms_norm
+ * (rmsnorm.py:48, engine.py:75).  cols % 8 == 0. */
+int q3_rmsnorm(const uint16_t *x, int ldx, const uint16_t *w, uint16_t *y, int ldy,
+               int rows, int cols, float eps, hipStream_t stream);
+
+/* sum = bf16(res + delta); y = RMSNorm(sum).  add_norm (fused.py:147).
+ * sum_out may equal res (in place). */
+int q3_add_rmsnorm(const uint16_t *res, const uint16_t *delta, uint16_t *sum_out,
+                   uint16_t *y, const uint16_t *w, int rows, int cols, float eps,
+                   hipStream_t stream);
+
+/* resid = embed[ids]; y = RMSNorm(resid).  F.embedding + the first input norm
+ * (engine.py:768,790). */
+int q3_embed_rmsnorm(const int64_t *ids, const uint16_t *embed, uint16_t *resid,
+                     uint16_t *y, const uint16_t *w, int rows, int cols, float eps,
+                     hipStream_t stream);
+
+/* Per-head QK RMSNorm + RoPE + KV-cache append for T tokens per sequence at
+ * absolute positions start..start+T-1 (start read from *start_pos on the
+ * device, plus start_offset).  qkv [B*T, ld_qkv] holds q | k | v;
+ * q_out [B*T, Hq, D]; cache_k/v [B, Hkv, capacity, D].
+ * norm_rope (fused.py:222) + kv_to_cache (fused.py:620). */
+int q3_qk_norm_rope_kv(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w,
+                       const uint16_t *k_norm_w, const uint16_t *cos_table,
+                       const uint16_t *sin_table, const int64_t *start_pos, int start_offset,
+                       uint16_t *q_out, uint16_t *cache_k, uint16_t *cache_v,
+                       int B, int T, int Hq, int Hkv, int D, int capacity, float eps,
+                       hipStream_t stream);
+
+/* Split-K GQA decode attention for the token at position *pos (one query per
+ * sequence), with the q/k RMSNorm + RoPE and the KV append of that token fused
+ * in.  qkv [B, ld_qkv] (q | k | v); cache_k/v [B, Hkv, capacity, 128].
+ * Writes per-split partials part_acc [B, Hq, splits, 128] (FP32, unnormalised)
+ * and part_ml [B, Hq, splits, 2] (running max, sum).  Finish with
+ * q3_attn_merge.  decode_attention_gqa / _split (fused.py:641-846). */
+int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w,
+                   const uint16_t *k_norm_w, const uint16_t *cos_table,
+                   const uint16_t *sin_table, const int64_t *pos,
+                   uint16_t *cache_k, uint16_t *cache_v, float *part_acc, float *part_ml,
+                   int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
+                   hipStream_t stream);
+/* Log-sum-exp merge of the splits: out [B, Hq*128] BF16 (fused.py:793-823). */
+int q3_attn_merge(const float *part_acc, const float *part_ml, uint16_t *out,
+                  int B, int Hq, int splits, hipStream_t stream);
+/* Splits q3_attn_decode uses for a cache of `capacity` keys. */
+int q3_attn_splits(int B, int Hkv, int capacity);
+
+/* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
+ * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /
+ * chunk mask (engine.py:263-280,777-787). */
+int q3_attn_prefill(const uint16_t *q, const uint16_t *cache_k, const uint16_t *cache_v,
+                    uint16_t *out, int B, int T, int start, int Hq, int Hkv,
+                    int capacity, float scale, hipStream_t stream);
+
+/* Greedy token from the argmax partials (first index on ties): tokens[b]
+ * (int64); when pos != NULL, *pos += 1 (the self-feeding graph's advance,
+ * engine.py:833-838). */
+int q3_argmax_finish(const float *part_val, const int *part_idx, int nparts, int B,
+                     int64_t *tokens, int64_t *pos, hipStream_t stream);
+/* Argmax over stored BF16 logits rows [B, V] (first index on ties); when
+ * pos != NULL, *pos += 1. */
+int q3_argmax_rows(const uint16_t *logits, int ld, int B, int V, int64_t *tokens,
+                   int64_t *pos, hipStream_t stream);
+
+/* hipGraph capture of everything enqueued on `stream` between begin and end
+ * (engine.py:1029-1065). */
+int q3_graph_begin(hipStream_t stream);
+int q3_graph_end(hipStream_t stream, void **exec_out);
+int q3_graph_launch(void *exec, hipStream_t stream);
+int q3_graph_destroy(void *exec);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q3_H */

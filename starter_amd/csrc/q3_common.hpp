@@ -1,0 +1,109 @@
+// Shared device helpers for the gfx950 Qwen3 decode kernels.
+//
+// BF16 values live in memory as raw uint16_t bits.  Every rounding to BF16 is
+// done explicitly with round-to-nearest-even on the FP32 bit pattern, which is
+// what a PyTorch BF16 op does after computing in FP32 (reference
+// engine/kernels/fused.py:8-13): each place the reference rounds, these
+// kernels round, and nowhere else.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#define Q3_WAVE 64
+
+// ------------------------------------------------------------ bf16 <-> fp32
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+// Low / high BF16 of a packed 32-bit word.
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even FP32 -> BF16 bits (inputs are finite here).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+// The FP32 value of f rounded to BF16.
+__device__ __forceinline__ float rbf(float f) { return __uint_as_float(f2bf(f) << 16); }
+
+__device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
+
+// --------------------------------------------------------------- reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, Q3_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, Q3_WAVE));
+    return v;
+}
+
+// Sum over the 16 lanes of a row (lanes 16r .. 16r+15).
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, Q3_WAVE);
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, Q3_WAVE));
+    return v;
+}
+
+// --------------------------------------------------------------- RMSNorm
+
+// 1 / sqrt(v) with a correctly rounded sqrt and divide (HIP's default FP32
+// sqrt and division are IEEE-rounded), matching torch.rsqrt on the CPU,
+// which is 1/sqrt vectorised.
+__device__ __forceinline__ float inv_rms(float sum_sq, int n, float eps) {
+    float var = sum_sq / (float)n;
+    return 1.0f / sqrtf(var + eps);
+}
+
+// Qwen3RMSNorm on one element: t = bf16(x * inv); y = bf16(w * t)
+// (reference engine/engine.py:84-88, rmsnorm.py:34-45).
+__device__ __forceinline__ uint32_t norm_elem(float x, float inv, float w) {
+    return f2bf(w * rbf(x * inv));
+}
+
+// ------------------------------------------------------------------ misc
+
+// 16-byte streaming load (non-temporal hint: weights are read once per step).
+__device__ __forceinline__ uint4 load_nt(const void* p) {
+    u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
+
+// 2 BF16 products accumulated into FP32: a.lo*b.lo + a.hi*b.hi + c.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), c, false);
+}
+
+__device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
+    c = dot2(a.x, b.x, c);
+    c = dot2(a.y, b.y, c);
+    c = dot2(a.z, b.z, c);
+    c = dot2(a.w, b.w, c);
+    return c;
+}
+
+// silu(g) rounded like F.silu on BF16: the FP32 value g / (1 + exp(-g)),
+// then one rounding (reference fused.py:107-111).
+__device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + expf(-g))); }
+
+#define Q3_CHECK_LAUNCH() return (int)hipGetLastError()

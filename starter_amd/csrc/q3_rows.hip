@@ -1,0 +1,258 @@
+// Row-wise kernels: RMSNorm (+ residual add / embedding gather), per-head
+// QK RMSNorm + RoPE + KV-cache append, and greedy argmax.
+//
+// Reference: engine/kernels/rmsnorm.py:21-71, engine/kernels/fused.py:115-251,
+// 553-638, engine/engine.py:75-109,768,790,833.  Cast placement follows those
+// files exactly: the FP32 normalised value rounds to BF16 before the gain
+// multiply, each RoPE product rounds before the sum, the residual sum rounds
+// before it is normalised.
+#include "q3_common.hpp"
+#include "q3.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int MAX_CHUNKS = 4;  // 16-byte chunks per thread kept in registers (cols <= 8192)
+
+// Block-wide sum (256 threads).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float sumsq8(uint4 v) {
+    float s = 0.f;
+    s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
+    s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
+    s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
+    s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
+    return s;
+}
+
+__device__ __forceinline__ uint4 norm8(uint4 v, uint4 g, float inv) {
+    uint4 o;
+    o.x = pack2(norm_elem(bflo(v.x), inv, bflo(g.x)), norm_elem(bfhi(v.x), inv, bfhi(g.x)));
+    o.y = pack2(norm_elem(bflo(v.y), inv, bflo(g.y)), norm_elem(bfhi(v.y), inv, bfhi(g.y)));
+    o.z = pack2(norm_elem(bflo(v.z), inv, bflo(g.z)), norm_elem(bfhi(v.z), inv, bfhi(g.z)));
+    o.w = pack2(norm_elem(bflo(v.w), inv, bflo(g.w)), norm_elem(bfhi(v.w), inv, bfhi(g.w)));
+    return o;
+}
+
+__device__ __forceinline__ uint32_t add2(uint32_t a, uint32_t b) {
+    return pack2(f2bf(bflo(a) + bflo(b)), f2bf(bfhi(a) + bfhi(b)));
+}
+
+enum { SRC_PLAIN = 0, SRC_ADD = 1, SRC_EMBED = 2 };
+
+// One row per workgroup.  SRC_PLAIN: x = a[row]; SRC_ADD: x = bf16(a + b),
+// written to sum_out; SRC_EMBED: x = embed[ids[row]], written to sum_out.
+template <int SRC>
+__global__ __launch_bounds__(THREADS) void rmsnorm_kernel(const bf16_t* a, int lda, const bf16_t* bsrc,
+                                                          const int64_t* ids, bf16_t* sum_out,
+                                                          const bf16_t* w, bf16_t* y, int ldy,
+                                                          int cols, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int chunks = cols >> 3;
+    const bf16_t* src;
+    if (SRC == SRC_EMBED) src = a + ids[row] * (int64_t)cols;
+    else src = a + (int64_t)row * lda;
+    uint4 xv[MAX_CHUNKS];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAX_CHUNKS; ++j) {
+        const int c = threadIdx.x + j * THREADS;
+        if (c < chunks) {
+            uint4 v = *reinterpret_cast<const uint4*>(src + c * 8);
+            if (SRC == SRC_ADD) {
+                uint4 d = *reinterpret_cast<const uint4*>(bsrc + (int64_t)row * cols + c * 8);
+                v = make_uint4(add2(v.x, d.x), add2(v.y, d.y), add2(v.z, d.z), add2(v.w, d.w));
+            }
+            if (SRC != SRC_PLAIN)
+                *reinterpret_cast<uint4*>(sum_out + (int64_t)row * cols + c * 8) = v;
+            xv[j] = v;
+            ss += sumsq8(v);
+        }
+    }
+    const float inv = inv_rms(block_sum(ss, red), cols, eps);
+#pragma unroll
+    for (int j = 0; j < MAX_CHUNKS; ++j) {
+        const int c = threadIdx.x + j * THREADS;
+        if (c < chunks) {
+            const uint4 g = *reinterpret_cast<const uint4*>(w + c * 8);
+            *reinterpret_cast<uint4*>(y + (int64_t)row * ldy + c * 8) = norm8(xv[j], g, inv);
+        }
+    }
+}
+
+// Per (token, head) RMSNorm over 128 then RoPE (lane l holds d = l and l+64).
+__device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w, const bf16_t* cosr,
+                                               const bf16_t* sinr, float eps, int lane, bf16_t* dst) {
+    const float lo = bf2f(x[lane]), hi = bf2f(x[lane + 64]);
+    const float inv = inv_rms(wave_sum(lo * lo + hi * hi), 128, eps);
+    const float n_lo = bf2f(norm_elem(lo, inv, bf2f(w[lane])));
+    const float n_hi = bf2f(norm_elem(hi, inv, bf2f(w[lane + 64])));
+    const float c_lo = bf2f(cosr[lane]), s_lo = bf2f(sinr[lane]);
+    const float c_hi = bf2f(cosr[lane + 64]), s_hi = bf2f(sinr[lane + 64]);
+    dst[lane] = (bf16_t)f2bf(rbf(n_lo * c_lo) + rbf(-n_hi * s_lo));
+    dst[lane + 64] = (bf16_t)f2bf(rbf(n_hi * c_hi) + rbf(n_lo * s_hi));
+}
+
+// grid (B*T): one workgroup per token, waves stride over Hq q-heads, Hkv
+// k-heads and Hkv v-heads.
+__global__ __launch_bounds__(THREADS) void qk_norm_rope_kv_kernel(
+    const bf16_t* qkv, int ld_qkv, const bf16_t* qw, const bf16_t* kw, const bf16_t* cos_t,
+    const bf16_t* sin_t, const int64_t* start_pos, int start_offset, bf16_t* q_out, bf16_t* cache_k,
+    bf16_t* cache_v, int T, int Hq, int Hkv, int capacity, float eps) {
+    const int bt = blockIdx.x, b = bt / T, t = bt % T;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int pos = (start_pos ? (int)*start_pos : 0) + start_offset + t;
+    if (pos < 0 || pos >= capacity) return;  // never write outside the cache
+    const bf16_t* row = qkv + (int64_t)bt * ld_qkv;
+    const bf16_t* cosr = cos_t + (int64_t)pos * 128;
+    const bf16_t* sinr = sin_t + (int64_t)pos * 128;
+    for (int h = wave; h < Hq + 2 * Hkv; h += THREADS / 64) {
+        if (h < Hq) {
+            head_norm_rope(row + h * 128, qw, cosr, sinr, eps, lane, q_out + ((int64_t)bt * Hq + h) * 128);
+        } else if (h < Hq + Hkv) {
+            const int kh = h - Hq;
+            bf16_t* dst = cache_k + (((int64_t)b * Hkv + kh) * capacity + pos) * 128;
+            head_norm_rope(row + h * 128, kw, cosr, sinr, eps, lane, dst);
+        } else {
+            const int vh = h - Hq - Hkv;
+            bf16_t* dst = cache_v + (((int64_t)b * Hkv + vh) * capacity + pos) * 128;
+            const bf16_t* src = row + h * 128;
+            dst[lane] = src[lane];
+            dst[lane + 64] = src[lane + 64];
+        }
+    }
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// grid (B): reduce argmax partials [nparts, B] -> tokens[b]; block 0 advances *pos.
+__global__ __launch_bounds__(THREADS) void argmax_finish_kernel(const float* pv, const int* pi, int nparts,
+                                                                int B, int64_t* tokens, int64_t* pos) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int p = threadIdx.x; p < nparts; p += THREADS) {
+        const float v = pv[p * B + b];
+        const int i = pi[p * B + b];
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float v = __shfl_xor(bv, o, Q3_WAVE);
+        const int i = __shfl_xor(bi, o, Q3_WAVE);
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+        tokens[b] = bi;
+        if (pos && b == 0) *pos += 1;
+    }
+}
+
+// grid (B): argmax over a stored BF16 logits row.
+__global__ __launch_bounds__(THREADS) void argmax_rows_kernel(const bf16_t* logits, int ld, int V,
+                                                              int64_t* tokens, int64_t* pos) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bf16_t* row = logits + (int64_t)b * ld;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += THREADS) {
+        const float v = bf2f(row[i]);
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float v = __shfl_xor(bv, o, Q3_WAVE);
+        const int i = __shfl_xor(bi, o, Q3_WAVE);
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+        tokens[b] = bi;
+        if (pos && b == 0) *pos += 1;
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+extern "C" int q3_rmsnorm(const bf16_t* x, int ldx, const bf16_t* w, bf16_t* y, int ldy, int rows, int cols,
+                          float eps, hipStream_t stream) {
+    if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || ldx % 8 || ldy % 8 ||
+        !aligned16(x) || !aligned16(y) || !aligned16(w))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel<SRC_PLAIN>, dim3(rows), dim3(THREADS), 0, stream, x, ldx, nullptr,
+                       nullptr, nullptr, w, y, ldy, cols, eps);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_add_rmsnorm(const bf16_t* res, const bf16_t* delta, bf16_t* sum_out, bf16_t* y,
+                              const bf16_t* w, int rows, int cols, float eps, hipStream_t stream) {
+    if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || !aligned16(res) ||
+        !aligned16(delta) || !aligned16(sum_out) || !aligned16(y) || !aligned16(w))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel<SRC_ADD>, dim3(rows), dim3(THREADS), 0, stream, res, cols, delta,
+                       nullptr, sum_out, w, y, cols, cols, eps);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_embed_rmsnorm(const int64_t* ids, const bf16_t* embed, bf16_t* resid, bf16_t* y,
+                                const bf16_t* w, int rows, int cols, float eps, hipStream_t stream) {
+    if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || !ids || !aligned16(embed) ||
+        !aligned16(resid) || !aligned16(y) || !aligned16(w))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel<SRC_EMBED>, dim3(rows), dim3(THREADS), 0, stream, embed, cols, nullptr,
+                       ids, resid, w, y, cols, cols, eps);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_qk_norm_rope_kv(const bf16_t* qkv, int ld_qkv, const bf16_t* q_norm_w,
+                                  const bf16_t* k_norm_w, const bf16_t* cos_table, const bf16_t* sin_table,
+                                  const int64_t* start_pos, int start_offset, bf16_t* q_out, bf16_t* cache_k,
+                                  bf16_t* cache_v, int B, int T, int Hq, int Hkv, int D, int capacity, float eps,
+                                  hipStream_t stream) {
+    if (B < 1 || T < 1 || Hq < 1 || Hkv < 1 || D != 128 || ld_qkv < (Hq + 2 * Hkv) * D || capacity < 1 ||
+        start_offset < 0 || (!start_pos && start_offset + T > capacity))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(B * T), dim3(THREADS), 0, stream, qkv, ld_qkv, q_norm_w,
+                       k_norm_w, cos_table, sin_table, start_pos, start_offset, q_out, cache_k, cache_v, T, Hq,
+                       Hkv, capacity, eps);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_argmax_finish(const float* part_val, const int* part_idx, int nparts, int B, int64_t* tokens,
+                                int64_t* pos, hipStream_t stream) {
+    if (nparts < 1 || B < 1 || !part_val || !part_idx || !tokens) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(THREADS), 0, stream, part_val, part_idx, nparts, B,
+                       tokens, pos);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_argmax_rows(const bf16_t* logits, int ld, int B, int V, int64_t* tokens, int64_t* pos,
+                              hipStream_t stream) {
+    if (B < 1 || V < 1 || ld < V || !logits || !tokens) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, tokens, pos);
+    Q3_CHECK_LAUNCH();
+}

@@ -1,0 +1,507 @@
+"""Qwen3-4B greedy decode on MI355X: the drop-in ``Engine`` of reference ``engine/engine.py``.
+
+API (identical to reference ``engine/engine.py:112-118,1069-1105``;
+``QWEN_ENGINE_CONTRACT.md`` "What you submit"):
+
+    eng = Engine(model_path)                 # local HF checkpoint directory
+    for step in eng.generate(input_ids, max_new_tokens):
+        ...                                  # list[int], one id per sequence
+
+``generate`` yields exactly ``max_new_tokens`` lists, greedy (first index on
+exact ties), every call starting from a clean state.  The private
+``_ensure_shape(batch, prompt, new)`` and ``_forward_prefill(ids, prompt)``
+keep the reference's names (its tests call them, reference
+``tests/test_equivalence.py:161-163``).
+
+Everything below the API is new: PyTorch-ROCm owns device memory and the
+stream; every operation of the forward is a gfx950 HIP kernel in
+``csrc/`` called through the C ABI of ``include/q3.h`` (``_lib``).  There is
+no eager or PyTorch fallback: if ``libq3.so`` is missing, construction fails.
+
+Device layout (bytes sized for one 288 GB HBM3E device):
+  * weights, BF16, [N, K] row-major: per layer ``qkv`` [6144, 2560]
+    (q | k | v rows), ``o`` [2560, 4096], ``gate_up`` [19456, 2560] with gate
+    and up rows interleaved (row 2j = gate_j, 2j+1 = up_j) so one wave or
+    tile owns both halves of its SwiGLU outputs, ``down`` [2560, 9728];
+    the tied embedding [151936, 2560] doubles as the LM head;
+  * KV cache: K and V each one allocation [layers, B, 8, capacity, 128] BF16,
+    capacity = prompt + new tokens (reference ``engine/engine.py:844-862``);
+  * RoPE tables [max(4096, capacity + 1), 128] BF16, computed on the host in
+    FP32 exactly as the reference does and uploaded once per shape.
+
+Decode step (one hipGraph, self-feeding like reference ``:805-839``), B <= 8:
+  gemv(embed+norm -> qkv) | attn(norm/rope/append + split-K GQA) | merge |
+  gemv(o, +residual) | gemv(norm -> gate_up -> SwiGLU) | gemv(down, +residual) |
+  gemv(norm -> qkv of the next layer) ... | gemv(norm -> lm_head -> argmax
+  partials) | argmax finish (token -> input buffer, pos += 1).
+For B > 8 the projections run on the MFMA GEMM with separate norm kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import time
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import call
+from .checkpoint import Qwen3Config, load_checkpoint
+
+DEVICE = "cuda:0"
+
+#: Prompt tokens (batch x prompt) per prefill chunk.  The reference caps a
+#: chunk at 16384 tokens for an 80 GB H100 (``engine/engine.py:34``); with
+#: 288 GB the full 131072-token prompts of the benchmark fit in one pass
+#: (~8 GB of activations).
+PREFILL_CHUNK_TOKENS = 131072
+
+#: Headroom kept free when sizing the KV cache.
+MEMORY_MARGIN_BYTES = 2 << 30
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _log(msg: str) -> None:
+    print(f"[engine] {msg}", flush=True)
+
+
+def rope_tables(theta: float, head_dim: int, length: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin [length, head_dim] in BF16, built in FP32 on the host.
+
+    Same formula and cast point as reference ``engine/engine.py:240-259``:
+    ``inv = 1/theta**(arange(0, D, 2)/D)`` (FP32), ``freqs = outer(pos, inv)``,
+    ``emb = cat(freqs, freqs)``, cos/sin in FP32, one cast to BF16.
+    """
+    exponent = torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim
+    inv_freq = 1.0 / (theta ** exponent)
+    pos = torch.arange(length, dtype=torch.int64).float()
+    emb = torch.cat((torch.outer(pos, inv_freq),) * 2, dim=-1)
+    return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+
+def _check_ids(input_ids, vocab: int) -> torch.Tensor:
+    """Prompt ids as an int64 [B, P] tensor; ids index the embedding table on the
+    device, so anything outside [0, vocab) is rejected here."""
+    ids = torch.tensor(input_ids, dtype=torch.int64)
+    if ids.dim() != 2 or ids.shape[0] == 0 or ids.shape[1] == 0:
+        raise ValueError("input_ids must be a non-empty list of equal-length, non-empty lists")
+    if int(ids.min()) < 0 or int(ids.max()) >= vocab:
+        raise ValueError(f"token ids must lie in [0, {vocab})")
+    return ids
+
+
+def _bf16(arr: np.ndarray, device: str) -> torch.Tensor:
+    host = torch.from_numpy(np.ascontiguousarray(arr).view(np.int16))
+    return host.to(device, non_blocking=False).view(torch.bfloat16)
+
+
+class Engine:
+    """Greedy Qwen3 decode engine; dimensions come from the checkpoint's config."""
+
+    def __init__(self, model_path: str) -> None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("Engine needs a ROCm GPU (gfx950); none is visible")
+        _lib.lib()  # fail now, not mid-generation, if the kernels are not built
+        self.device = torch.device(DEVICE)
+        torch.cuda.set_device(self.device)
+        self.started = time.monotonic()
+        cfg, tensors = load_checkpoint(model_path)
+        self.cfg: Qwen3Config = cfg
+        self.LAYERS = cfg.num_hidden_layers
+        self.HIDDEN = cfg.hidden_size
+        self.INTER = cfg.intermediate_size
+        self.HEADS = cfg.num_attention_heads
+        self.KV_HEADS = cfg.num_key_value_heads
+        self.HEAD_DIM = cfg.head_dim
+        self.VOCAB = cfg.vocab_size
+        self.EPS = float(cfg.rms_norm_eps)
+        self.THETA = float(cfg.rope_theta)
+        self.SCALE = self.HEAD_DIM ** -0.5
+        if self.HEAD_DIM != 128 or self.HEADS != 4 * self.KV_HEADS:
+            raise ValueError("kernels are built for head_dim 128 and 4 query heads per KV head")
+        if self.HIDDEN % 64 or self.INTER % 64 or self.HIDDEN > _lib.GEMV_MAX_NORM_K:
+            raise ValueError("hidden and intermediate sizes must be multiples of 64; hidden <= 4096")
+        self.q_size = self.HEADS * self.HEAD_DIM
+        self.kv_size = self.KV_HEADS * self.HEAD_DIM
+        self.qkv_size = self.q_size + 2 * self.kv_size
+        self.stream = torch.cuda.Stream(device=self.device)
+
+        dev = DEVICE
+        self.embed = _bf16(tensors["model.embed_tokens.weight"], dev)
+        self.lm_head = (self.embed if cfg.tie_word_embeddings
+                        else _bf16(tensors["lm_head.weight"], dev))
+        self.final_norm = _bf16(tensors["model.norm.weight"], dev)
+        self.layers = []
+        for i in range(self.LAYERS):
+            p = f"model.layers.{i}."
+            qkv = np.concatenate([tensors[p + "self_attn.q_proj.weight"],
+                                  tensors[p + "self_attn.k_proj.weight"],
+                                  tensors[p + "self_attn.v_proj.weight"]], axis=0)
+            gate, up = tensors[p + "mlp.gate_proj.weight"], tensors[p + "mlp.up_proj.weight"]
+            gate_up = np.stack([gate, up], axis=1).reshape(2 * self.INTER, self.HIDDEN)
+            self.layers.append({
+                "in_ln": _bf16(tensors[p + "input_layernorm.weight"], dev),
+                "post_ln": _bf16(tensors[p + "post_attention_layernorm.weight"], dev),
+                "q_norm": _bf16(tensors[p + "self_attn.q_norm.weight"], dev),
+                "k_norm": _bf16(tensors[p + "self_attn.k_norm.weight"], dev),
+                "qkv": _bf16(qkv, dev),
+                "o": _bf16(tensors[p + "self_attn.o_proj.weight"], dev),
+                "gate_up": _bf16(gate_up, dev),
+                "down": _bf16(tensors[p + "mlp.down_proj.weight"], dev),
+            })
+        del tensors
+        torch.cuda.synchronize()
+
+        self.rope_len = 0
+        self.cos_table = self.sin_table = None
+        self._grow_rope(4096)
+
+        self.batch = 0
+        self.capacity = 0
+        self.cache_k = self.cache_v = None
+        self.graph = None
+        self.keep_logits = False
+        self._prefill_bufs = {}
+        _log(f"loaded {self.LAYERS} layers in {time.monotonic() - self.started:.1f}s; "
+             f"qkv and gate_up packed")
+
+    # ------------------------------------------------------------------ rope
+
+    def _grow_rope(self, length: int) -> None:
+        if length <= self.rope_len:
+            return
+        length = max(length, 4096)
+        cos, sin = rope_tables(self.THETA, self.HEAD_DIM, length)
+        self.cos_table = cos.to(self.device)
+        self.sin_table = sin.to(self.device)
+        self.rope_len = length
+
+    # --------------------------------------------------------------- helpers
+
+    @property
+    def _s(self) -> int:
+        return self.stream.cuda_stream
+
+    def _empty(self, *shape, dtype=torch.bfloat16):
+        return torch.empty(*shape, dtype=dtype, device=self.device)
+
+    # ------------------------------------------------------------ shape prep
+
+    def _ensure_shape(self, batch: int, seq_len: int, max_new_tokens: int) -> None:
+        """(Re)build caches, decode buffers and the decode graph for (batch, capacity).
+
+        Keyed on (batch, prompt + new) like reference ``engine/engine.py:843-880``,
+        so a different prompt/new split with the same capacity reuses the graph:
+        nothing in it depends on the prompt length (positions are device data).
+        """
+        capacity = seq_len + max_new_tokens
+        if self.batch == batch and self.capacity == capacity and self.graph is not None:
+            return
+        _log(f"building for batch={batch} capacity={capacity}")
+        self._release_graph()
+        self.cache_k = self.cache_v = None
+        self._prefill_bufs = {}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+        self._grow_rope(capacity + 1)
+        L, Hkv, D = self.LAYERS, self.KV_HEADS, self.HEAD_DIM
+        cache_bytes = 2 * L * batch * Hkv * capacity * D * 2
+        free, _ = torch.cuda.mem_get_info(self.device)
+        if cache_bytes + MEMORY_MARGIN_BYTES > free:
+            raise MemoryError(f"KV cache needs {cache_bytes / 2**30:.1f} GiB; "
+                              f"{free / 2**30:.1f} GiB free")
+        self.cache_k = torch.zeros(L, batch, Hkv, capacity, D, dtype=torch.bfloat16, device=self.device)
+        self.cache_v = torch.zeros_like(self.cache_k)
+        self.batch, self.capacity = batch, capacity
+
+        B, H, V = batch, self.HIDDEN, self.VOCAB
+        self.splits = call("q3_attn_splits", B, Hkv, capacity)
+        self.g_token = torch.zeros(B, dtype=torch.int64, device=self.device)
+        self.g_pos = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.resid = self._empty(B, H)
+        self.nbuf = self._empty(B, H)
+        self.qkv_buf = self._empty(B, self.qkv_size)
+        self.attn_out = self._empty(B, self.q_size)
+        self.act = self._empty(B, self.INTER)
+        self.part_acc = self._empty(B, self.HEADS, self.splits, D, dtype=torch.float32)
+        self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
+        self.small = B <= _lib.GEMV_MAX_M
+        if self.small:
+            self.lm_parts = call("q3_gemv_partials", B, V, H)
+            self.part_val = self._empty(self.lm_parts, B, dtype=torch.float32)
+            self.part_idx = self._empty(self.lm_parts, B, dtype=torch.int32)
+        self.logits = self._empty(B, V)
+        self._capture()
+
+    def _release_graph(self) -> None:
+        if self.graph is not None:
+            torch.cuda.synchronize()
+            call("q3_graph_destroy", self.graph)
+            self.graph = None
+
+    def __del__(self):
+        try:
+            self._release_graph()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+    # --------------------------------------------------------------- decode
+
+    def _enqueue_decode(self) -> None:
+        """One self-feeding decode step on ``self.stream`` (reference ``_forward_decode``)."""
+        s = self._s
+        B, H, I, V = self.batch, self.HIDDEN, self.INTER, self.VOCAB
+        D, Hq, Hkv, C = self.HEAD_DIM, self.HEADS, self.KV_HEADS, self.capacity
+        layer_stride = self.cache_k[0].numel() * 2
+        kc0, vc0 = self.cache_k.data_ptr(), self.cache_v.data_ptr()
+        tok, pos = _ptr(self.g_token), _ptr(self.g_pos)
+        resid, qkv, attn, act, nbuf = (_ptr(self.resid), _ptr(self.qkv_buf), _ptr(self.attn_out),
+                                       _ptr(self.act), _ptr(self.nbuf))
+        for i, L in enumerate(self.layers):
+            if self.small:
+                if i == 0:
+                    call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
+                         resid, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
+                         None, None, s)
+                else:
+                    call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["in_ln"]), self.EPS, None,
+                         _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
+                         None, None, s)
+            else:
+                if i == 0:
+                    call("q3_embed_rmsnorm", tok, _ptr(self.embed), resid, nbuf, _ptr(L["in_ln"]), B, H,
+                         self.EPS, s)
+                else:
+                    call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
+                call("q3_gemm", nbuf, H, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv,
+                     self.qkv_size, s)
+            call("q3_attn_decode", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
+                 _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
+                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml), B, Hq, Hkv, C,
+                 self.splits, self.EPS, self.SCALE, s)
+            call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+            if self.small:
+                call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
+                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, s)
+                call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["post_ln"]), self.EPS, None,
+                     _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, s)
+                call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
+                     B, H, I, _lib.EPI_RESID, resid, H, None, None, s)
+            else:
+                call("q3_gemm", attn, self.q_size, _ptr(L["o"]), B, H, self.q_size, _lib.EPI_RESID,
+                     resid, H, s)
+                call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), nbuf, H, B, H, self.EPS, s)
+                call("q3_gemm", nbuf, H, _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, s)
+                call("q3_gemm", act, I, _ptr(L["down"]), B, H, I, _lib.EPI_RESID, resid, H, s)
+        if self.small:
+            epi = _lib.EPI_STORE_ARGMAX if self.keep_logits else _lib.EPI_ARGMAX
+            call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(self.final_norm), self.EPS, None,
+                 _ptr(self.lm_head), B, V, H, epi, _ptr(self.logits), V, _ptr(self.part_val),
+                 _ptr(self.part_idx), s)
+            call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok,
+                 pos, s)
+        else:
+            call("q3_rmsnorm", resid, H, _ptr(self.final_norm), nbuf, H, B, H, self.EPS, s)
+            call("q3_gemm", nbuf, H, _ptr(self.lm_head), B, V, H, _lib.EPI_STORE, _ptr(self.logits), V, s)
+            call("q3_argmax_rows", _ptr(self.logits), V, B, V, tok, pos, s)
+
+    def _capture(self) -> None:
+        """Warm every kernel eagerly, then record one decode step as a hipGraph.
+
+        Reference ``engine/engine.py:1029-1059``.  A failed capture raises: the
+        engine has no eager decode mode to fall back to.
+        """
+        with torch.cuda.stream(self.stream):
+            for _ in range(2):
+                self.g_pos.fill_(max(0, self.capacity - 2))
+                self._enqueue_decode()
+            self.g_pos.zero_()
+            self.g_token.zero_()
+        self.stream.synchronize()
+        call("q3_graph_begin", self._s)
+        try:
+            self._enqueue_decode()
+        except Exception:
+            exec_ptr = ctypes.c_void_p()
+            _lib.lib().q3_graph_end(self._s, ctypes.byref(exec_ptr))
+            if exec_ptr.value:
+                call("q3_graph_destroy", exec_ptr.value)
+            raise
+        exec_ptr = ctypes.c_void_p()
+        call("q3_graph_end", self._s, ctypes.byref(exec_ptr))
+        self.graph = exec_ptr.value
+        _log(f"decode graph captured (batch={self.batch}, splits={self.splits})")
+
+    def _decode_step(self) -> torch.Tensor:
+        """Replay the captured step: g_token <- next token, g_pos += 1."""
+        call("q3_graph_launch", self.graph, self._s)
+        return self.g_token
+
+    # -------------------------------------------------------------- prefill
+
+    def _prefill_buffers(self, rows: int) -> dict:
+        bufs = self._prefill_bufs.get(rows)
+        if bufs is None:
+            self._prefill_bufs = {}
+            bufs = {
+                "resid": self._empty(rows, self.HIDDEN),
+                "n": self._empty(rows, self.HIDDEN),
+                "qkv": self._empty(rows, self.qkv_size),
+                "q": self._empty(rows, self.q_size),
+                "a": self._empty(rows, self.q_size),
+                "act": self._empty(rows, self.INTER),
+            }
+            self._prefill_bufs[rows] = bufs
+        return bufs
+
+    def _forward_prefill(self, ids: torch.Tensor, seq_len: int) -> torch.Tensor:
+        """Consume the prompt ``ids [B, P]``; return the last position's logits [B, 1, V].
+
+        Reference ``engine/engine.py:738-803``: chunks of ``PREFILL_CHUNK_TOKENS
+        // B`` tokens per sequence, causal within the chunk and over every
+        earlier key; the cache is written for every prompt position.
+        """
+        B = ids.shape[0]
+        if B != self.batch or seq_len > self.capacity or ids.shape[1] != seq_len:
+            raise ValueError(f"prefill of {tuple(ids.shape)} does not fit the cache "
+                             f"(batch {self.batch}, capacity {self.capacity})")
+        if int(ids.min()) < 0 or int(ids.max()) >= self.VOCAB:
+            raise ValueError(f"token ids must lie in [0, {self.VOCAB})")
+        ids = ids.to(self.device, torch.int64)
+        chunk = seq_len
+        if B * seq_len > PREFILL_CHUNK_TOKENS:
+            chunk = max(1, PREFILL_CHUNK_TOKENS // B)
+        H, I, D, Hq, Hkv, C = self.HIDDEN, self.INTER, self.HEAD_DIM, self.HEADS, self.KV_HEADS, self.capacity
+        layer_stride = self.cache_k[0].numel() * 2
+        kc0, vc0 = self.cache_k.data_ptr(), self.cache_v.data_ptr()
+        s = self._s
+        with torch.cuda.stream(self.stream):
+            for start in range(0, seq_len, chunk):
+                stop = min(start + chunk, seq_len)
+                T = stop - start
+                M = B * T
+                bufs = self._prefill_buffers(B * min(chunk, seq_len))
+                chunk_ids = ids[:, start:stop].contiguous()
+                resid, n, qkv, q, a, act = (_ptr(bufs[k]) for k in ("resid", "n", "qkv", "q", "a", "act"))
+                for i, L in enumerate(self.layers):
+                    if i == 0:
+                        call("q3_embed_rmsnorm", _ptr(chunk_ids), _ptr(self.embed), resid, n,
+                             _ptr(L["in_ln"]), M, H, self.EPS, s)
+                    else:
+                        call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), n, H, M, H, self.EPS, s)
+                    call("q3_gemm", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
+                         self.qkv_size, s)
+                    call("q3_qk_norm_rope_kv", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
+                         _ptr(self.cos_table), _ptr(self.sin_table), None, start, q,
+                         kc0 + i * layer_stride, vc0 + i * layer_stride, B, T, Hq, Hkv, D, C, self.EPS, s)
+                    call("q3_attn_prefill", q, kc0 + i * layer_stride, vc0 + i * layer_stride, a, B, T,
+                         start, Hq, Hkv, C, self.SCALE, s)
+                    call("q3_gemm", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
+                         resid, H, s)
+                    call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), n, H, M, H, self.EPS, s)
+                    call("q3_gemm", n, H, _ptr(L["gate_up"]), M, 2 * I, H, _lib.EPI_SWIGLU, act, I, s)
+                    call("q3_gemm", act, I, _ptr(L["down"]), M, H, I, _lib.EPI_RESID, resid, H, s)
+                last = bufs["resid"][(T - 1):]  # row T-1 of sequence 0; sequences are T rows apart
+            # The final norm is applied on the last position only, then the tied LM head
+            # (reference :800-803: the last layer's closing norm uses final_norm_w).
+            logits = self._empty(B, self.VOCAB)
+            if B <= _lib.GEMV_MAX_M:
+                call("q3_gemv", _lib.X_NORM, _ptr(last), T * H, None, _ptr(self.final_norm), self.EPS, None,
+                     _ptr(self.lm_head), B, self.VOCAB, H, _lib.EPI_STORE, _ptr(logits), self.VOCAB,
+                     None, None, s)
+            else:
+                n_last = self._empty(B, H)
+                call("q3_rmsnorm", _ptr(last), T * H, _ptr(self.final_norm), _ptr(n_last), H, B, H,
+                     self.EPS, s)
+                call("q3_gemm", _ptr(n_last), H, _ptr(self.lm_head), B, self.VOCAB, H, _lib.EPI_STORE,
+                     _ptr(logits), self.VOCAB, s)
+        return logits.view(B, 1, self.VOCAB)
+
+    # ------------------------------------------------------------- generate
+
+    @torch.inference_mode()
+    def generate(self, input_ids: list[list[int]], max_new_tokens: int):
+        """Greedy continuation; yields ``max_new_tokens`` lists of one id per sequence.
+
+        Reference ``engine/engine.py:1069-1105``: prefill, argmax, then one graph
+        replay per further token with one step of device-to-host lookahead.
+        """
+        if max_new_tokens <= 0:
+            return
+        ids = _check_ids(input_ids, self.VOCAB)
+        batch, seq_len = ids.shape
+        self._ensure_shape(batch, seq_len, max_new_tokens)
+        ids = ids.to(self.device)
+
+        # No state carries between calls: positions restart at the prompt length,
+        # and only slots below the running position are ever read.
+        self.stream.wait_stream(torch.cuda.current_stream())
+        logits = self._forward_prefill(ids, seq_len)
+        with torch.cuda.stream(self.stream):
+            call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
+                 self._s)
+            self.g_pos.fill_(seq_len)
+        host = torch.empty(batch, dtype=torch.int64, pin_memory=True)
+        done = torch.cuda.Event()
+        pending = False
+        for step in range(max_new_tokens):
+            if not pending:
+                self.stream.synchronize()
+                out = self.g_token.cpu()
+            else:
+                done.synchronize()
+                out = host.clone()
+            if step + 1 < max_new_tokens:
+                self._decode_step()
+                with torch.cuda.stream(self.stream):
+                    host.copy_(self.g_token, non_blocking=True)
+                    done.record(self.stream)
+                pending = True
+            else:
+                pending = False
+            yield out.tolist()
+
+    # -------------------------------------------------------- diagnostics
+
+    @torch.inference_mode()
+    def trace_logits(self, input_ids: list[list[int]], max_new_tokens: int):
+        """Tokens plus the BF16 logits each step's ids were chosen from.
+
+        Not part of the reference API: parity tests use it to compare per-step
+        logits with the CPU oracle.  Returns (steps, logits [N, B, V] on the CPU).
+        """
+        ids = _check_ids(input_ids, self.VOCAB)
+        batch, seq_len = ids.shape
+        self.keep_logits = True
+        self.graph_key_reset()
+        self._ensure_shape(batch, seq_len, max_new_tokens)
+        logits = self._forward_prefill(ids.to(self.device), seq_len)
+        with torch.cuda.stream(self.stream):
+            call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
+                 self._s)
+            self.g_pos.fill_(seq_len)
+        self.stream.synchronize()
+        steps, kept = [self.g_token.cpu().tolist()], [logits.view(batch, -1).cpu()]
+        for _ in range(max_new_tokens - 1):
+            self._decode_step()
+            self.stream.synchronize()
+            steps.append(self.g_token.cpu().tolist())
+            kept.append(self.logits.cpu())
+        self.keep_logits = False
+        self.graph_key_reset()
+        return steps, torch.stack(kept)
+
+    def graph_key_reset(self) -> None:
+        """Force the next ``_ensure_shape`` to rebuild (e.g. after toggling keep_logits)."""
+        self._release_graph()
+        self.batch = self.capacity = 0
+
+
+def _env_flag(name: str) -> bool:
+    return os.environ.get(name, "") not in ("", "0")

@@ -1,0 +1,71 @@
+"""The C ABI: libq3.so loads and exports every entry point include/q3.h declares.
+
+No compute calls here (there is no GPU in the CPU suite); argument checks that
+fail before any launch are exercised, since they return an error code without
+touching the device.
+"""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from starter_amd import _lib
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def header_functions() -> list[str]:
+    text = (ROOT / "include" / "q3.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q3_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = header_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_python_binding_covers_the_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_header_constants_match_binding():
+    text = (ROOT / "include" / "q3.h").read_text()
+    consts = dict(re.findall(r"#define (Q3_\w+) (\d+)", text))
+    for name in ("X_PLAIN", "X_NORM", "X_EMBED_NORM", "EPI_STORE", "EPI_RESID", "EPI_SWIGLU",
+                 "EPI_ARGMAX", "EPI_STORE_ARGMAX", "GEMV_MAX_M", "GEMV_MAX_NORM_K"):
+        assert int(consts["Q3_" + name]) == getattr(_lib, name), name
+
+
+def test_error_string():
+    assert _lib.error_string(0)
+    assert _lib.error_string(1)  # hipErrorInvalidValue
+
+
+def test_bad_arguments_raise_without_launching():
+    # M = 0 and K not a multiple of 8 are rejected before any device work.
+    with pytest.raises(RuntimeError, match="q3_gemv failed"):
+        _lib.call("q3_gemv", 0, None, 0, None, None, 0.0, None, None, 0, 4, 8, 0, None, 0, None, None, None)
+    with pytest.raises(RuntimeError, match="q3_gemm failed"):
+        _lib.call("q3_gemm", None, 0, None, 4, 4, 60, 0, None, 0, None)
+    with pytest.raises(RuntimeError, match="q3_attn_decode failed"):
+        _lib.call("q3_attn_decode", None, 0, None, None, None, None, None, None, None, None, None,
+                  1, 32, 7, 64, 1, 1e-6, 0.1, None)
+
+
+def test_attention_splits_policy():
+    # One split per 256 keys once the launch has >= 512 workgroups, else per 128.
+    assert _lib.call("q3_attn_splits", 1, 8, 64) == 1
+    assert _lib.call("q3_attn_splits", 1, 8, 1536) == 12
+    assert _lib.call("q3_attn_splits", 64, 8, 2176) == 9
+    assert _lib.call("q3_attn_splits", 8, 8, 16512) == 65
+
+
+def test_gemv_partials():
+    assert _lib.call("q3_gemv_partials", 1, 151936, 2560) == 151936 // 4 // 4
+    assert _lib.call("q3_gemv_partials", 8, 151936, 2560) == 151936 // 2 // 4

@@ -1,0 +1,342 @@
+"""Kernel parity on the GPU, each launch through the C ABI (libq3.so).
+
+Each kernel is compared with the CPU oracle's function for the same op
+(oracle/qwen3_cpu.py, itself pinned by tests/test_oracle.py) or, for the
+projections, a float32 reference of the same dot products.  Tolerances, written
+per test:
+  * element-wise ops (norm, RoPE, residual add, SwiGLU, KV append): bit-exact
+    except where an FP32 reduction (the RMS of a row) sums in another order,
+    which may move one element by one BF16 ulp -- at most 1e-3 of elements;
+  * projections: |gpu - ref| <= 1 BF16 ulp of the FP32 reference's rounding,
+    with >= 97% of elements bit-equal (only the summation order differs);
+  * attention: max |gpu - oracle| <= 1e-2 + 1e-2 |oracle| (P rounds to BF16
+    before P.V, as in reference fused.py:699-701).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qwen3_cpu as oc
+from starter_amd import _lib
+from starter_amd._lib import call
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def P(t):
+    return None if t is None else t.data_ptr()
+
+
+def S():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rnd(shape, scale=1.0, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def ulps(a: torch.Tensor, b: torch.Tensor) -> np.ndarray:
+    """|a - b| in units of b's BF16 spacing."""
+    a64, b64 = a.float().numpy().astype(np.float64), b.float().numpy().astype(np.float64)
+    spacing = np.exp2(np.floor(np.log2(np.maximum(np.abs(b64), 2.0 ** -126))) - 7)
+    return np.abs(a64 - b64) / spacing
+
+
+def assert_nearly_exact(got, want, frac=1e-3, max_ulp=1):
+    u = ulps(got.cpu(), want.cpu())
+    assert u.max() <= max_ulp, f"max {u.max()} ulp"
+    assert (u > 0).mean() <= frac, f"{(u > 0).mean():.2e} of elements differ"
+
+
+# ------------------------------------------------------------------ norms
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 320), (5, 2560), (3, 4096)])
+def test_rmsnorm(rows, cols):
+    x = rnd((rows, cols), 2.0, 1)
+    w = (1 + rnd((cols,), 0.2, 2).float()).to(torch.bfloat16)
+    y = torch.empty(rows, cols, dtype=torch.bfloat16, device=DEV)
+    call("q3_rmsnorm", P(x.to(DEV)), cols, P(w.to(DEV)), P(y), cols, rows, cols, 1e-6, S())
+    torch.cuda.synchronize()
+    assert_nearly_exact(y, oc.rms_norm(x, w, 1e-6))
+
+
+def test_add_rmsnorm_and_embed():
+    rows, cols = 9, 2560
+    r, d = rnd((rows, cols), 1.0, 3), rnd((rows, cols), 1.0, 4)
+    w = (1 + rnd((cols,), 0.2, 5).float()).to(torch.bfloat16)
+    rd, dd, wd = r.to(DEV), d.to(DEV), w.to(DEV)
+    s = torch.empty_like(rd)
+    y = torch.empty_like(rd)
+    call("q3_add_rmsnorm", P(rd), P(dd), P(s), P(y), P(wd), rows, cols, 1e-6, S())
+    torch.cuda.synchronize()
+    want_s = r + d
+    assert torch.equal(s.cpu(), want_s)  # the residual sum rounds exactly like a BF16 add
+    assert_nearly_exact(y, oc.rms_norm(want_s, w, 1e-6))
+    # In place (sum_out == res).
+    call("q3_add_rmsnorm", P(rd), P(dd), P(rd), P(y), P(wd), rows, cols, 1e-6, S())
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), want_s)
+
+    table = rnd((50, cols), 1.0, 6)
+    ids = torch.tensor([3, 49, 0, 3], dtype=torch.int64)
+    resid = torch.empty(4, cols, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty_like(resid)
+    call("q3_embed_rmsnorm", P(ids.to(DEV)), P(table.to(DEV)), P(resid), P(y), P(wd), 4, cols, 1e-6, S())
+    torch.cuda.synchronize()
+    assert torch.equal(resid.cpu(), table[ids])
+    assert_nearly_exact(y, oc.rms_norm(table[ids], w, 1e-6))
+
+
+# ------------------------------------------------------- qk norm + rope + kv
+
+
+@pytest.mark.parametrize("B,T,start", [(1, 1, 0), (2, 5, 3), (3, 17, 40)])
+def test_qk_norm_rope_kv(B, T, start):
+    Hq, Hkv, D, C = 8, 2, 128, 64
+    width = (Hq + 2 * Hkv) * D
+    qkv = rnd((B * T, width), 1.5, 7)
+    qw = (1 + rnd((D,), 0.2, 8).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 9).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, 4096)
+    ck = torch.zeros(B, Hkv, C, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    q_out = torch.empty(B * T, Hq, D, dtype=torch.bfloat16, device=DEV)
+    call("q3_qk_norm_rope_kv", P(qkv.to(DEV)), width, P(qw.to(DEV)), P(kw.to(DEV)), P(cos.to(DEV)),
+         P(sin.to(DEV)), None, start, P(q_out), P(ck), P(cv), B, T, Hq, Hkv, D, C, 1e-6, S())
+    torch.cuda.synchronize()
+    x = qkv.view(B, T, Hq + 2 * Hkv, D)
+    c = cos[start:start + T].view(1, T, 1, D)
+    s_ = sin[start:start + T].view(1, T, 1, D)
+    want_q = oc.apply_rope(oc.rms_norm(x[:, :, :Hq], qw, 1e-6), c, s_)
+    want_k = oc.apply_rope(oc.rms_norm(x[:, :, Hq:Hq + Hkv], kw, 1e-6), c, s_)
+    assert_nearly_exact(q_out.view(B, T, Hq, D), want_q, frac=2e-3, max_ulp=2)
+    got_k = ck.cpu()
+    assert_nearly_exact(got_k[:, :, start:start + T].transpose(1, 2), want_k, frac=2e-3, max_ulp=2)
+    assert torch.equal(cv.cpu()[:, :, start:start + T].transpose(1, 2), x[:, :, Hq + Hkv:])
+    # Nothing outside the written slots.
+    mask = torch.ones(C, dtype=torch.bool)
+    mask[start:start + T] = False
+    assert torch.all(got_k[:, :, mask] == 0) and torch.all(cv.cpu()[:, :, mask] == 0)
+
+
+# ------------------------------------------------------------ projections
+
+
+def ref_linear(x, w):
+    return (x.float() @ w.float().T)
+
+
+def check_projection(got, want_f32, frac=0.03):
+    want = want_f32.to(torch.bfloat16)
+    u = ulps(got.cpu(), want)
+    assert u.max() <= 1.0, f"max {u.max()} ulp"
+    assert (u > 0).mean() <= frac, f"{(u > 0).mean():.3f} differ"
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("N,K", [(1536, 320), (320, 1024), (2560, 2560), (2560, 9728)])
+def test_gemv_plain_store(M, N, K):
+    x, w = rnd((M, K), 1.0, M), rnd((N, K), 0.02, N + K)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemv", _lib.X_PLAIN, P(x.to(DEV)), K, None, None, 0.0, None, P(w.to(DEV)), M, N, K,
+         _lib.EPI_STORE, P(y), N, None, None, S())
+    torch.cuda.synchronize()
+    check_projection(y, ref_linear(x, w))
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_gemv_norm_resid_swiglu(M):
+    K, N, I = 2560, 1024, 512
+    src = rnd((M, K), 1.0, 11)
+    g = (1 + rnd((K,), 0.2, 12).float()).to(torch.bfloat16)
+    w = rnd((N, K), 0.02, 13)
+    n_ref = oc.rms_norm(src, g, 1e-6)
+    # NORM prologue + STORE
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    srcd, gd, wd = src.to(DEV), g.to(DEV), w.to(DEV)
+    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wd), M, N, K, _lib.EPI_STORE, P(y), N,
+         None, None, S())
+    torch.cuda.synchronize()
+    check_projection(y, ref_linear(n_ref, w), frac=0.05)
+    # RESID epilogue: y = bf16(res + bf16(acc)), in place.
+    res = rnd((M, N), 1.0, 14)
+    resd = res.to(DEV)
+    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wd), M, N, K, _lib.EPI_RESID, P(resd),
+         N, None, None, S())
+    torch.cuda.synchronize()
+    want = res + ref_linear(n_ref, w).to(torch.bfloat16)
+    u = ulps(resd.cpu(), want)
+    assert u.max() <= 1.0 and (u > 0).mean() < 0.03
+    # SWIGLU epilogue on interleaved (gate, up) rows.
+    wg, wu = rnd((I, K), 0.02, 15), rnd((I, K), 0.02, 16)
+    wgu = torch.stack([wg, wu], 1).reshape(2 * I, K)
+    act = torch.empty(M, I, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wgu.to(DEV)), M, 2 * I, K,
+         _lib.EPI_SWIGLU, P(act), I, None, None, S())
+    torch.cuda.synchronize()
+    gate = ref_linear(n_ref, wg).to(torch.bfloat16)
+    up = ref_linear(n_ref, wu).to(torch.bfloat16)
+    want = oc.swiglu(gate, up)
+    u = ulps(act.cpu(), want)
+    assert u.max() <= 3 and (u > 0).mean() < 0.06
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_gemv_embed_norm_and_argmax(M):
+    V, K = 4096, 2560
+    table = rnd((V, K), 0.02, 21)
+    g = (1 + rnd((K,), 0.2, 22).float()).to(torch.bfloat16)
+    ids = torch.randint(0, V, (M,), generator=torch.Generator().manual_seed(M))
+    td, gd = table.to(DEV), g.to(DEV)
+    resid = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(M, V, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemv", _lib.X_EMBED_NORM, P(td), K, P(ids.to(DEV)), P(gd), 1e-6, P(resid), P(td), M, V, K,
+         _lib.EPI_STORE, P(y), V, None, None, S())
+    torch.cuda.synchronize()
+    assert torch.equal(resid.cpu(), table[ids])
+    n_ref = oc.rms_norm(table[ids], g, 1e-6)
+    check_projection(y, ref_linear(n_ref, table), frac=0.05)
+    # Fused argmax partials + finish == argmax of the stored logits (first index on ties).
+    nparts = call("q3_gemv_partials", M, V, K)
+    pv = torch.empty(nparts, M, dtype=torch.float32, device=DEV)
+    pi = torch.empty(nparts, M, dtype=torch.int32, device=DEV)
+    y2 = torch.empty_like(y)
+    call("q3_gemv", _lib.X_NORM, P(resid), K, None, P(gd), 1e-6, None, P(td), M, V, K, _lib.EPI_STORE_ARGMAX,
+         P(y2), V, P(pv), P(pi), S())
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    pos = torch.tensor([5], dtype=torch.int64, device=DEV)
+    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), P(pos), S())
+    torch.cuda.synchronize()
+    assert torch.equal(y2.cpu(), y.cpu())
+    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist()
+    assert pos.item() == 6
+
+
+def test_argmax_rows_ties():
+    V = 5000
+    x = torch.zeros(3, V, dtype=torch.bfloat16)
+    x[0, [7, 4000]] = 3.0
+    x[1, :] = -1.0
+    x[2, [4999, 12, 13]] = 2.5
+    tok = torch.empty(3, dtype=torch.int64, device=DEV)
+    pos = torch.zeros(1, dtype=torch.int64, device=DEV)
+    call("q3_argmax_rows", P(x.to(DEV)), V, 3, V, P(tok), P(pos), S())
+    torch.cuda.synchronize()
+    assert tok.cpu().tolist() == [7, 0, 12] and pos.item() == 1
+
+
+@pytest.mark.parametrize("M", [1, 9, 16, 17, 40, 64, 100, 300])
+@pytest.mark.parametrize("N,K", [(320, 1024), (1536, 320), (2560, 2560)])
+def test_gemm(M, N, K):
+    x, w = rnd((M, K), 1.0, M + 1), rnd((N, K), 0.02, N + K + 1)
+    xd, wd = x.to(DEV), w.to(DEV)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(y), N, S())
+    torch.cuda.synchronize()
+    check_projection(y, ref_linear(x, w))
+    res = rnd((M, N), 1.0, 5)
+    resd = res.to(DEV)
+    call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_RESID, P(resd), N, S())
+    act = torch.empty(M, N // 2, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_SWIGLU, P(act), N // 2, S())
+    torch.cuda.synchronize()
+    ref = ref_linear(x, w).to(torch.bfloat16)
+    u = ulps(resd.cpu(), res + ref)
+    assert u.max() <= 1.0 and (u > 0).mean() < 0.03
+    want = oc.swiglu(ref[:, 0::2], ref[:, 1::2])
+    u = ulps(act.cpu(), want)
+    assert u.max() <= 3 and (u > 0).mean() < 0.06
+
+
+# -------------------------------------------------------------- attention
+
+
+def attention_oracle(q, ck, cv, length, scale):
+    """q [B, Hq, D] -> [B, Hq, D] over keys 0..length-1 (oracle SDPA, BF16)."""
+    out = oc.attention(q.unsqueeze(2), ck[:, :, :length], cv[:, :, :length], scale, length - 1)
+    return out[:, :, 0]
+
+
+@pytest.mark.parametrize("B,C,pos,splits", [(1, 64, 0, 1), (1, 64, 31, 1), (2, 64, 32, 1), (1, 300, 200, 3),
+                                            (3, 300, 299, 5), (2, 1536, 1100, 12), (1, 1536, 1535, 12),
+                                            (2, 700, 255, 40)])
+def test_attn_decode(B, C, pos, splits):
+    Hq, Hkv, D = 32, 8, 128
+    width = (Hq + 2 * Hkv) * D
+    qkv = rnd((B, width), 1.5, pos + 1)
+    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    ck = rnd((B, Hkv, C, D), 1.0, 4)
+    cv = rnd((B, Hkv, C, D), 1.0, 5)
+    ckd, cvd = ck.to(DEV), cv.to(DEV)
+    pacc = torch.empty(B, Hq, splits, D, dtype=torch.float32, device=DEV)
+    pml = torch.empty(B, Hq, splits, 2, dtype=torch.float32, device=DEV)
+    out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+    posd = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    call("q3_attn_decode", P(qkv.to(DEV)), width, P(qw.to(DEV)), P(kw.to(DEV)), P(cos.to(DEV)), P(sin.to(DEV)),
+         P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
+    call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
+    torch.cuda.synchronize()
+    x = qkv.view(B, 1, Hq + 2 * Hkv, D)
+    c, s_ = cos[pos].view(1, 1, 1, D), sin[pos].view(1, 1, 1, D)
+    q = oc.apply_rope(oc.rms_norm(x[:, :, :Hq], qw, 1e-6), c, s_)[:, 0]
+    k = oc.apply_rope(oc.rms_norm(x[:, :, Hq:Hq + Hkv], kw, 1e-6), c, s_)[:, 0]
+    ck_ref, cv_ref = ck.clone(), cv.clone()
+    ck_ref[:, :, pos] = k
+    cv_ref[:, :, pos] = x[:, 0, Hq + Hkv:]
+    # The append: exactly one slot changes.
+    got_k, got_v = ckd.cpu(), cvd.cpu()
+    assert torch.equal(got_v, cv_ref)
+    other = torch.ones(C, dtype=torch.bool)
+    other[pos] = False
+    assert torch.equal(got_k[:, :, other], ck[:, :, other])
+    assert_nearly_exact(got_k[:, :, pos], k, frac=5e-3, max_ulp=2)
+    want = attention_oracle(q, ck_ref, cv_ref, pos + 1, D ** -0.5).float()
+    got = out.cpu().view(B, Hq, D).float()
+    err = (got - want).abs()
+    assert (err <= 1e-2 + 1e-2 * want.abs()).all(), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("B,T,start", [(1, 1, 0), (2, 37, 0), (1, 64, 0), (2, 20, 30), (3, 50, 13)])
+def test_attn_prefill(B, T, start):
+    Hq, Hkv, D = 32, 8, 128
+    C = start + T + 5
+    q = rnd((B * T, Hq, D), 1.0, T)
+    ck = rnd((B, Hkv, C, D), 1.0, T + 1)
+    cv = rnd((B, Hkv, C, D), 1.0, T + 2)
+    out = torch.empty(B * T, Hq * D, dtype=torch.bfloat16, device=DEV)
+    call("q3_attn_prefill", P(q.to(DEV)), P(ck.to(DEV)), P(cv.to(DEV)), P(out), B, T, start, Hq, Hkv, C,
+         D ** -0.5, S())
+    torch.cuda.synchronize()
+    qt = q.view(B, T, Hq, D).transpose(1, 2)
+    want = oc.attention(qt, ck[:, :, :start + T], cv[:, :, :start + T], D ** -0.5, start)
+    want = want.transpose(1, 2).reshape(B * T, Hq * D).float()
+    got = out.cpu().float()
+    err = (got - want).abs()
+    assert (err <= 1e-2 + 1e-2 * want.abs()).all(), f"max err {err.max():.3e}"
+
+
+def test_graph_capture_replays_self_feeding_step():
+    """A captured argmax_finish advances pos on every replay (the decode loop's feed)."""
+    stream = torch.cuda.Stream()
+    pv = torch.tensor([[1.0], [3.0], [3.0]], device=DEV)
+    pi = torch.tensor([[5], [9], [2]], dtype=torch.int32, device=DEV)
+    tok = torch.zeros(1, dtype=torch.int64, device=DEV)
+    pos = torch.zeros(1, dtype=torch.int64, device=DEV)
+    import ctypes
+    torch.cuda.synchronize()
+    call("q3_graph_begin", stream.cuda_stream)
+    call("q3_argmax_finish", P(pv), P(pi), 3, 1, P(tok), P(pos), stream.cuda_stream)
+    ex = ctypes.c_void_p()
+    call("q3_graph_end", stream.cuda_stream, ctypes.byref(ex))
+    for _ in range(3):
+        call("q3_graph_launch", ex.value, stream.cuda_stream)
+    stream.synchronize()
+    call("q3_graph_destroy", ex.value)
+    assert tok.item() == 2 and pos.item() == 3

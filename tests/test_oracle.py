@@ -1,0 +1,193 @@
+"""Pins the CPU oracle (oracle/qwen3_cpu.py) before anything is checked against it.
+
+Three kinds of evidence, chosen so a plausible slip (a cast in the wrong
+place, a sign in rotate_half, a transposed projection, a wrong KV head) fails:
+  * HF fixtures (tests/golden/*.npz, written by make_golden.py from
+    transformers' Qwen3ForCausalLM): token streams and logits on a tiny model
+    in fp32 and bf16 over the reference test's cases (reference
+    tests/test_equivalence.py:208-220), and on the full seeded Qwen3-4B at
+    config 1;
+  * float64 closed forms with the BF16 roundings applied by hand;
+  * identities: RoPE at position 0, a single key, argmax first-index ties.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from make_golden import TINY_CASES
+from oracle import qwen3_cpu as oc
+from starter_amd.checkpoint import load_checkpoint
+
+GOLD = {}
+
+
+def golden(name):
+    from conftest import GOLDEN
+    if name not in GOLD:
+        GOLD[name] = np.load(GOLDEN / f"{name}.npz")
+    return GOLD[name]
+
+
+def bits_to_f64(t: torch.Tensor) -> np.ndarray:
+    return t.float().numpy().astype(np.float64)
+
+
+# ------------------------------------------------------------ closed forms
+
+
+def test_rms_norm_cast_placement():
+    """y = bf16(w * bf16(x * rsqrt(mean(x^2)+eps))): the inner rounding is kept."""
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(64, 2560, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(2560, generator=g)).to(torch.bfloat16)
+    got = bits_to_f64(oc.rms_norm(x, w, 1e-6))
+    xf = x.float().numpy().astype(np.float64)
+    var = (xf.astype(np.float32) ** 2).astype(np.float64).mean(-1, keepdims=True)
+    inv = 1.0 / np.sqrt(var.astype(np.float32) + np.float32(1e-6))
+    t = oc.bf16_round((xf * inv).astype(np.float32))
+    want = oc.bf16_round(t * w.float().numpy())
+    mism = got != want
+    # The FP32 mean may differ from the float64-then-float32 one by an ulp, which
+    # can flip a rounding; anything more is a formula error.
+    assert mism.mean() < 1e-3
+    # Rounding once at the end instead would disagree far more often.
+    wrong = oc.bf16_round(xf * inv * w.float().numpy())
+    assert (got != wrong).mean() > 0.05
+
+
+def test_rms_norm_zero_and_constant_rows():
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    x[1] = 2.0
+    w = torch.ones(128, dtype=torch.bfloat16)
+    y = oc.rms_norm(x, w, 1e-6).float()
+    assert torch.all(y[0] == 0)
+    assert torch.all(y[1] == torch.tensor(2.0 / np.sqrt(4.0 + 1e-6)).to(torch.bfloat16).float())
+
+
+def test_rope_tables_against_float64():
+    cos, sin = oc.rope_tables(5e6, 128, 4096)
+    c64, s64 = oc.reference_tables_f64(5e6, 128, 4096)
+    # FP32 angles (pos * inv_freq) lose precision at large positions; what is
+    # pinned is agreement to within the BF16 spacing plus the FP32 angle error.
+    ang_err = 4096 * 2.0 ** -24 * 4
+    assert np.abs(cos.float().numpy() - c64).max() < 2 ** -8 + ang_err
+    assert np.abs(sin.float().numpy() - s64).max() < 2 ** -8 + ang_err
+    assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
+    # Both halves repeat the same angles (emb = cat(freqs, freqs)).
+    assert torch.equal(cos[:, :64], cos[:, 64:]) and torch.equal(sin[:, :64], sin[:, 64:])
+
+
+def test_rope_position_zero_is_identity_and_rotation_sign():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 128, generator=g).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, 128, 16)
+    assert torch.equal(oc.apply_rope(x, cos[0], sin[0]), x)
+    # Position 1, lane 0 (angle 1 rad): lo' = r(r(lo*c) + r(-hi*s)), hi' = r(r(hi*c) + r(lo*s)).
+    y = oc.apply_rope(x, cos[1], sin[1]).float().numpy()
+    lo, hi = x[:, 0].float().numpy(), x[:, 64].float().numpy()
+    c, s = float(cos[1, 0]), float(sin[1, 0])
+    want_lo = oc.bf16_round(oc.bf16_round(lo * c) + oc.bf16_round(-hi * s))
+    want_hi = oc.bf16_round(oc.bf16_round(hi * c) + oc.bf16_round(lo * s))
+    assert np.array_equal(y[:, 0], want_lo) and np.array_equal(y[:, 64], want_hi)
+
+
+def test_swiglu_two_roundings():
+    g = torch.Generator().manual_seed(2)
+    gate = (torch.randn(4096, generator=g) * 4).to(torch.bfloat16)
+    up = torch.randn(4096, generator=g).to(torch.bfloat16)
+    got = oc.swiglu(gate, up).float().numpy()
+    gf = gate.float().numpy().astype(np.float64)
+    a = oc.bf16_round(gf / (1 + np.exp(-gf)))
+    want = oc.bf16_round(a * up.float().numpy())
+    assert (got != want).mean() < 2e-3  # exp differs from float64 by < 1 ulp of FP32
+
+
+def test_linear_matches_float64_dot():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 2560, generator=g).to(torch.bfloat16)
+    w = (torch.randn(257, 2560, generator=g) * 0.02).to(torch.bfloat16)
+    got = oc.linear(x, w).float().numpy()
+    exact = x.float().numpy().astype(np.float64) @ w.float().numpy().astype(np.float64).T
+    want = oc.bf16_round(exact)
+    ulp = np.vectorize(oc.ulp_bf16)(want)
+    assert np.all(np.abs(got - want) <= ulp)
+    assert (got == want).mean() > 0.98
+
+
+def test_attention_against_brute_force():
+    g = torch.Generator().manual_seed(4)
+    B, Hq, Hkv, T, D = 2, 8, 2, 9, 128
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    out = oc.attention(q, k, v, D ** -0.5, T - 1).float().numpy()
+    for b in range(B):
+        for h in range(Hq):
+            kv = h // (Hq // Hkv)  # query head h reads KV head h // 4
+            want = oc.softmax_attention_f64(q[b, h, 0].float().numpy(), k[b, kv].float().numpy(),
+                                            v[b, kv].float().numpy(), D ** -0.5)
+            assert np.abs(out[b, h, 0] - want).max() < 2e-2
+    # A single key returns that key's value exactly.
+    one = oc.attention(q, k[:, :, :1], v[:, :, :1], D ** -0.5, 0)
+    assert torch.equal(one[:, :4, 0], v[:, :1, 0].expand(B, 4, D))
+
+
+def test_chunked_prefill_mask_is_causal():
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, D, S, T = 1, 4, 1, 128, 6, 3
+    q = torch.randn(B, Hq, T, D, generator=g)
+    k = torch.randn(B, Hkv, S + T, D, generator=g)
+    v = torch.randn(B, Hkv, S + T, D, generator=g)
+    out = oc.attention(q, k, v, D ** -0.5, S)
+    for i in range(T):
+        want = oc.softmax_attention_f64(q[0, 0, i].numpy(), k[0, 0, :S + i + 1].numpy(),
+                                        v[0, 0, :S + i + 1].numpy(), D ** -0.5)
+        assert np.abs(out[0, 0, i].numpy() - want).max() < 1e-5
+
+
+def test_argmax_first_index_on_ties():
+    x = torch.tensor([[1.0, 3.0, 3.0, 2.0], [5.0, 5.0, 5.0, 5.0]]).to(torch.bfloat16)
+    assert oc.argmax_first(x).tolist() == [1, 0]
+
+
+# ------------------------------------------------------------- HF fixtures
+
+
+@pytest.mark.parametrize("tag,dtype", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_oracle_matches_hf_tiny(tiny_ckpt, tag, dtype):
+    cfg, tensors = load_checkpoint(tiny_ckpt)
+    g = golden(f"tiny_{tag}")
+    orc = oc.Qwen3Oracle(cfg, tensors, dtype)
+    for name, b, p, n, chunk in TINY_CASES:
+        ids = g[f"{name}/ids"]
+        steps, logits = orc.generate(ids.tolist(), n, keep_logits=True,
+                                     chunk=(chunk // b) if chunk else None)
+        assert np.array_equal(np.array(steps), g[f"{name}/tokens"]), name
+        want = g[f"{name}/logits"]
+        for i, lg in enumerate(logits):
+            d = np.abs(lg.float().numpy() - want[i]).max()
+            # Unchunked cases reproduce HF bit for bit; a chunked prefill reorders
+            # the attention sums (the mask path), a few BF16 ulps of logit at most.
+            assert d <= (0.0 if not chunk else 0.07), (name, i, d)
+    # Prefill logits of a separate prompt (reference tests/test_equivalence.py:145-171).
+    orc.reset(2, 44)
+    got = orc.prefill(torch.from_numpy(g["prefill/ids"]))
+    assert np.abs(got.float().numpy() - g["prefill/logits"]).max() == 0.0
+
+
+@pytest.mark.slow
+def test_oracle_matches_hf_config1(full_ckpt):
+    """Full seeded Qwen3-4B, B=1, P=32, 32 steps: the oracle is HF's native path."""
+    cfg, tensors = load_checkpoint(full_ckpt)
+    g = golden("config1_bf16")
+    orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
+    del tensors
+    steps, logits = orc.generate(g["ids"].tolist(), len(g["tokens"]), keep_logits=True)
+    assert [s[0] for s in steps] == g["tokens"].tolist()
+    first = logits[0][0].float().numpy()
+    last = logits[-1][0].float().numpy()
+    assert np.array_equal(first, g["logits_first"])
+    assert np.array_equal(last, g["logits_last"])
+    subset = np.stack([lg[0].float().numpy()[g["subset"]] for lg in logits])
+    assert np.array_equal(subset, g["subset_logits"])
