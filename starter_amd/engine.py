@@ -373,7 +373,11 @@ class Engine:
                              f"(batch {self.batch}, capacity {self.capacity})")
         if int(ids.min()) < 0 or int(ids.max()) >= self.VOCAB:
             raise ValueError(f"token ids must lie in [0, {self.VOCAB})")
-        ids = ids.to(self.device, torch.int64)
+        if ids.is_cuda:
+            # Made on the caller's stream, read on ours: keep the block alive until
+            # our stream is done with it.
+            self.stream.wait_stream(torch.cuda.current_stream())
+            ids.record_stream(self.stream)
         chunk = seq_len
         if B * seq_len > PREFILL_CHUNK_TOKENS:
             chunk = max(1, PREFILL_CHUNK_TOKENS // B)
@@ -382,6 +386,7 @@ class Engine:
         kc0, vc0 = self.cache_k.data_ptr(), self.cache_v.data_ptr()
         s = self._s
         with torch.cuda.stream(self.stream):
+            ids = ids.to(self.device, torch.int64)
             for start in range(0, seq_len, chunk):
                 stop = min(start + chunk, seq_len)
                 T = stop - start
@@ -437,11 +442,9 @@ class Engine:
         ids = _check_ids(input_ids, self.VOCAB)
         batch, seq_len = ids.shape
         self._ensure_shape(batch, seq_len, max_new_tokens)
-        ids = ids.to(self.device)
 
         # No state carries between calls: positions restart at the prompt length,
         # and only slots below the running position are ever read.
-        self.stream.wait_stream(torch.cuda.current_stream())
         logits = self._forward_prefill(ids, seq_len)
         with torch.cuda.stream(self.stream):
             call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
@@ -470,25 +473,32 @@ class Engine:
     # -------------------------------------------------------- diagnostics
 
     @torch.inference_mode()
-    def trace_logits(self, input_ids: list[list[int]], max_new_tokens: int):
+    def trace_logits(self, input_ids: list[list[int]], max_new_tokens: int,
+                     forced: list[list[int]] | None = None):
         """Tokens plus the BF16 logits each step's ids were chosen from.
 
         Not part of the reference API: parity tests use it to compare per-step
-        logits with the CPU oracle.  Returns (steps, logits [N, B, V] on the CPU).
+        logits with the CPU oracle.  With ``forced`` (one list of B ids per
+        step), step i+1 is fed ``forced[i]`` instead of the engine's own choice
+        (teacher forcing, as the contest's judge replays a stream).  Returns
+        (steps, logits [N, B, V] on the CPU).
         """
         ids = _check_ids(input_ids, self.VOCAB)
         batch, seq_len = ids.shape
         self.keep_logits = True
         self.graph_key_reset()
         self._ensure_shape(batch, seq_len, max_new_tokens)
-        logits = self._forward_prefill(ids.to(self.device), seq_len)
+        logits = self._forward_prefill(ids, seq_len)
         with torch.cuda.stream(self.stream):
             call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
                  self._s)
             self.g_pos.fill_(seq_len)
         self.stream.synchronize()
         steps, kept = [self.g_token.cpu().tolist()], [logits.view(batch, -1).cpu()]
-        for _ in range(max_new_tokens - 1):
+        for i in range(max_new_tokens - 1):
+            if forced is not None:
+                self.g_token.copy_(torch.tensor(forced[i], dtype=torch.int64))
+                torch.cuda.synchronize()
             self._decode_step()
             self.stream.synchronize()
             steps.append(self.g_token.cpu().tolist())

@@ -104,10 +104,10 @@ def make_tiny(tmp: pathlib.Path) -> None:
         g = np.random.Generator(np.random.PCG64(77))
         arrays["reset/first"] = g.integers(0, TINY.vocab_size, (2, 24), dtype=np.int64)
         arrays["reset/second"] = g.integers(0, TINY.vocab_size, (2, 24), dtype=np.int64)
-        arrays["reset/tokens"], _ = baseline_loop(model, arrays["reset/second"], 5)
+        arrays["reset/tokens"], arrays["reset/logits"] = baseline_loop(model, arrays["reset/second"], 5)
         arrays["reuse/first"] = g.integers(0, TINY.vocab_size, (2, 30), dtype=np.int64)
         arrays["reuse/second"] = g.integers(0, TINY.vocab_size, (2, 26), dtype=np.int64)
-        arrays["reuse/tokens"], _ = baseline_loop(model, arrays["reuse/second"], 10)
+        arrays["reuse/tokens"], arrays["reuse/logits"] = baseline_loop(model, arrays["reuse/second"], 10)
         # reference tests/test_equivalence.py:145-171: prefill logits of a 2x40 prompt.
         arrays["prefill/ids"] = g.integers(0, TINY.vocab_size, (2, 40), dtype=np.int64)
         with torch.inference_mode():

@@ -3,12 +3,25 @@
 Mirrors reference tests/test_equivalence.py (the cases at :208-220, the reset
 test :120-142, shape reuse :174-197 and the prefill logit delta :145-171), but
 in BF16 -- the precision the engine runs in -- against fixtures written from
-transformers' Qwen3ForCausalLM (tests/golden/make_golden.py), and on the full
-seeded Qwen3-4B at config 1.
+transformers' Qwen3ForCausalLM on the CPU (tests/golden/make_golden.py), and
+on the full seeded Qwen3-4B at BASELINE config 1.
 
-Bar: token ids equal to HF's at every step up to the
-first near-tie (HF's top-2 logit gap < 1e-2); per-step logits within
-max-abs 5e-2 of HF's on those steps.
+The bar, per sequence (the contest's quality rule, reference
+QWEN_ENGINE_CONTRACT.md "The quality rule", with a margin of 2*TOL instead of
+2.0 logits):
+  * until the engine's token first differs from HF's, every step's logits are
+    within TOL (max-abs over the vocabulary) of HF's;
+  * at that first differing step, the engine's token has an HF logit within
+    2*TOL of HF's maximum -- i.e. HF's top-2 gap there was below 2*TOL, a
+    near-tie at the precision any reordered BF16 forward has;
+  * teacher-forced on HF's tokens (config 1), every step satisfies both.
+
+TOL is the measured noise floor of a reorder-only GPU forward, not a free
+parameter: on the seeded Qwen3-4B, PyTorch's own GPU path (hipBLASLt GEMMs,
+FP32 attention) differs from HF-on-CPU by max-abs 0.18 / mean 0.029 logits at
+step 0, and the engine by 0.16 / 0.028; on the 3-layer test model the engine
+stays within 0.05.  BF16 logits near 4 are 0.031 apart, so a 1-2 ulp HF gap
+is a tie for any implementation that sums in another order.
 """
 
 import numpy as np
@@ -17,13 +30,14 @@ import torch
 
 from make_golden import TINY_CASES
 from oracle import qwen3_cpu as oc
+from oracle.compare import check_stream
 from starter_amd import engine as engine_mod
 from starter_amd.checkpoint import load_checkpoint
 
 pytestmark = pytest.mark.gpu
 
-NEAR_TIE = 1e-2
-LOGIT_TOL = 5e-2
+TOL_TINY = 0.06   # 3 layers, hidden 320
+TOL_FULL = 0.25   # 36 layers, hidden 2560 (measured noise floor 0.16-0.18)
 
 
 def golden(name):
@@ -31,33 +45,9 @@ def golden(name):
     return np.load(GOLDEN / f"{name}.npz")
 
 
-def first_near_tie(logits: np.ndarray) -> int:
-    """First step (axis 0) at which any row's top-2 gap is below NEAR_TIE."""
-    srt = np.sort(logits, axis=-1)
-    gap = srt[..., -1] - srt[..., -2]
-    if gap.ndim == 2:
-        gap = gap.min(-1)
-    bad = np.nonzero(gap < NEAR_TIE)[0]
-    return int(bad[0]) if len(bad) else logits.shape[0]
-
-
 @pytest.fixture(scope="module")
 def tiny_engine(tiny_ckpt):
     return engine_mod.Engine(str(tiny_ckpt))
-
-
-def compare_case(got_steps, want_tokens, want_logits, got_logits=None):
-    # Tokens must agree strictly before the first near-tie; logits are comparable
-    # through it (step i's logits depend only on tokens 0..i-1).
-    stop = first_near_tie(want_logits)
-    got = np.array(got_steps)
-    assert got.shape == want_tokens.shape
-    assert np.array_equal(got[:stop], want_tokens[:stop]), (
-        f"tokens differ before the first near-tie (step {stop}): {got[:stop].T} vs {want_tokens[:stop].T}")
-    if got_logits is not None:
-        d = np.abs(got_logits[:stop + 1] - want_logits[:stop + 1]).max()
-        assert d <= LOGIT_TOL, f"logit max-abs {d:.3e} on steps 0..{stop}"
-    return stop
 
 
 @pytest.mark.parametrize("case", TINY_CASES, ids=[c[0] for c in TINY_CASES])
@@ -75,38 +65,44 @@ def test_tiny_cases_match_hf(tiny_engine, case):
         engine_mod.PREFILL_CHUNK_TOKENS = saved
     assert len(got) == n and all(len(s) == b for s in got)
     assert got == steps  # the streaming generator and the traced loop agree
-    compare_case(got, g[f"{name}/tokens"], g[f"{name}/logits"], logits.float().numpy())
+    firsts = check_stream(got, logits.float().numpy(), g[f"{name}/tokens"], g[f"{name}/logits"], TOL_TINY)
+    print(f"{name}: first divergence per row {firsts} of {n}")
 
 
 def test_cache_reset_across_calls(tiny_engine):
     g = golden("tiny_bf16")
     list(tiny_engine.generate(g["reset/first"].tolist(), 5))
     got = list(tiny_engine.generate(g["reset/second"].tolist(), 5))
-    assert got == g["reset/tokens"].tolist()
+    _, logits = tiny_engine.trace_logits(g["reset/second"].tolist(), 5)
+    check_stream(got, logits.float().numpy(), g["reset/tokens"], g["reset/logits"], TOL_TINY)
 
 
 def test_shape_reuse_at_equal_capacity(tiny_engine):
     g = golden("tiny_bf16")
     list(tiny_engine.generate(g["reuse/first"].tolist(), 6))          # capacity 36
     got = list(tiny_engine.generate(g["reuse/second"].tolist(), 10))  # capacity 36 again
-    assert got == g["reuse/tokens"].tolist()
+    _, logits = tiny_engine.trace_logits(g["reuse/second"].tolist(), 10)
+    check_stream(got, logits.float().numpy(), g["reuse/tokens"], g["reuse/logits"], TOL_TINY)
 
 
 def test_prefill_logit_delta(tiny_engine):
     g = golden("tiny_bf16")
     ids = torch.from_numpy(g["prefill/ids"])
     tiny_engine._ensure_shape(2, 40, 4)
-    mine = tiny_engine._forward_prefill(ids.cuda(), 40)
+    mine = tiny_engine._forward_prefill(ids, 40)
     tiny_engine.stream.synchronize()
     want = g["prefill/logits"]
     delta = np.abs(mine.float().cpu().numpy()[:, 0] - want).max()
-    assert delta < LOGIT_TOL, delta
+    # reference tests/test_equivalence.py:166: delta < 0.05 * max(|logit|, 1)
+    assert delta < min(TOL_TINY, 0.05 * max(np.abs(want).max(), 1.0)), delta
 
 
 def test_yield_contract(tiny_engine):
     out = list(tiny_engine.generate([[1, 2, 3]], 1))
     assert len(out) == 1 and len(out[0]) == 1
     assert list(tiny_engine.generate([[1, 2, 3]], 0)) == []
+    with pytest.raises(ValueError):
+        list(tiny_engine.generate([[1, 2, 512]], 2))  # id outside the vocabulary
 
 
 @pytest.mark.parametrize("batch", [9, 12])
@@ -118,11 +114,11 @@ def test_large_batch_path_matches_oracle(tiny_engine, tiny_ckpt, batch):
     ids = rng.integers(0, cfg.vocab_size, (batch, 21)).tolist()
     want, want_logits = orc.generate(ids, 6, keep_logits=True)
     steps, logits = tiny_engine.trace_logits(ids, 6)
-    compare_case(steps, np.array(want), torch.stack(want_logits).float().numpy(), logits.float().numpy())
+    check_stream(steps, logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
 
 
 def test_batch_rows_are_independent(tiny_engine):
-    """A row's tokens do not depend on the other rows of the batch."""
+    """A row's tokens do not depend on the other rows of the batch (bit-identical)."""
     rng = np.random.Generator(np.random.PCG64(3))
     ids = rng.integers(0, 512, (3, 17)).tolist()
     together = list(tiny_engine.generate(ids, 8))
@@ -131,22 +127,39 @@ def test_batch_rows_are_independent(tiny_engine):
         assert [s[r] for s in together] == [s[0] for s in alone]
 
 
+def test_deterministic_replays(tiny_engine):
+    """Same prompt twice: identical streams (no atomics, fixed reduction orders)."""
+    ids = [[5, 6, 7, 8, 9, 10, 11]] * 2
+    assert list(tiny_engine.generate(ids, 12)) == list(tiny_engine.generate(ids, 12))
+
+
 def test_config1_full_model_matches_hf(full_ckpt):
     """Seeded Qwen3-4B, B=1, P=32, 32 greedy tokens."""
     g = golden("config1_bf16")
     eng = engine_mod.Engine(str(full_ckpt))
     ids = g["ids"].tolist()
-    got = [s[0] for s in eng.generate(ids, 32)]
-    steps, logits = eng.trace_logits(ids, 32)
-    assert got == [s[0] for s in steps]
-    lg = logits[:, 0].float().numpy()
-    stop = int(np.nonzero(g["top2_gap"] < NEAR_TIE)[0][0]) if (g["top2_gap"] < NEAR_TIE).any() else 32
     want = g["tokens"].tolist()
-    assert got[:stop] == want[:stop], (stop, got, want)
-    d_first = np.abs(lg[0] - g["logits_first"]).max()
-    d_subset = np.abs(lg[:stop + 1][:, g["subset"]] - g["subset_logits"][:stop + 1]).max()
-    print(f"config1: tokens equal through step {stop}; logit max-abs first {d_first:.3e}, "
-          f"subset {d_subset:.3e}", flush=True)
-    assert d_first <= LOGIT_TOL and d_subset <= LOGIT_TOL
-    if got == want:
-        assert np.abs(lg[-1] - g["logits_last"]).max() <= LOGIT_TOL
+    got = [s[0] for s in eng.generate(ids, 32)]
+
+    def hf_logit(i, tok):
+        hit = np.nonzero(g["top_ids"][i] == tok)[0]
+        return g["top_logits"][i][hit[0]] if len(hit) else -np.inf
+
+    # Free-running: first divergence is a near-tie of HF's.
+    d = next((i for i in range(32) if got[i] != want[i]), 32)
+    if d < 32:
+        short = g["top_logits"][d][0] - hf_logit(d, got[d])
+        assert short <= 2 * TOL_FULL, (d, got[d], want[d], short)
+    # Teacher-forced on HF's tokens: every step within TOL and a near-argmax choice.
+    steps, logits = eng.trace_logits(ids, 32, forced=[[t] for t in want])
+    lg = logits[:, 0].float().numpy()
+    first = np.abs(lg[0] - g["logits_first"]).max()
+    last = np.abs(lg[-1] - g["logits_last"]).max()
+    sub = np.abs(lg[:, g["subset"]] - g["subset_logits"]).max(axis=1)
+    shorts = [g["top_logits"][i][0] - hf_logit(i, steps[i][0]) for i in range(32)]
+    print(f"config1: free-running tokens equal through step {d - 1}; teacher-forced logit "
+          f"max-abs first {first:.3f} last {last:.3f} subset {sub.max():.3f}; "
+          f"argmax matches HF at {sum(s[0] == w for s, w in zip(steps, want))}/32 steps, "
+          f"worst shortfall {max(shorts):.4f}", flush=True)
+    assert first <= TOL_FULL and last <= TOL_FULL and sub.max() <= TOL_FULL
+    assert max(shorts) <= 2 * TOL_FULL

@@ -7,8 +7,10 @@ per test:
   * element-wise ops (norm, RoPE, residual add, SwiGLU, KV append): bit-exact
     except where an FP32 reduction (the RMS of a row) sums in another order,
     which may move one element by one BF16 ulp -- at most 1e-3 of elements;
-  * projections: |gpu - ref| <= 1 BF16 ulp of the FP32 reference's rounding,
-    with >= 97% of elements bit-equal (only the summation order differs);
+  * projections: |gpu - exact| <= 1 BF16 ulp + 2^-17 sum|x*w| against the
+    float64 dot product, >= 97% of elements rounding exactly like it (only the
+    summation order differs); the fused prologues and epilogues are checked
+    bit-exactly against the unfused kernels they replace;
   * attention: max |gpu - oracle| <= 1e-2 + 1e-2 |oracle| (P rounds to BF16
     before P.V, as in reference fused.py:699-701).
 """
@@ -28,6 +30,27 @@ DEV = "cuda:0"
 
 def P(t):
     return None if t is None else t.data_ptr()
+
+
+_KEEP = []
+
+
+def dv(t):
+    """Device copy that stays alive for the rest of the test.
+
+    A pointer taken from a temporary (``P(x.to(DEV))``) would dangle: the
+    caching allocator hands the freed block to the next temporary.
+    """
+    d = t.to(DEV)
+    _KEEP.append(d)
+    return d
+
+
+@pytest.fixture(autouse=True)
+def _release_device_copies():
+    yield
+    torch.cuda.synchronize()
+    _KEEP.clear()
 
 
 def S():
@@ -60,7 +83,7 @@ def test_rmsnorm(rows, cols):
     x = rnd((rows, cols), 2.0, 1)
     w = (1 + rnd((cols,), 0.2, 2).float()).to(torch.bfloat16)
     y = torch.empty(rows, cols, dtype=torch.bfloat16, device=DEV)
-    call("q3_rmsnorm", P(x.to(DEV)), cols, P(w.to(DEV)), P(y), cols, rows, cols, 1e-6, S())
+    call("q3_rmsnorm", P(dv(x)), cols, P(dv(w)), P(y), cols, rows, cols, 1e-6, S())
     torch.cuda.synchronize()
     assert_nearly_exact(y, oc.rms_norm(x, w, 1e-6))
 
@@ -86,7 +109,7 @@ def test_add_rmsnorm_and_embed():
     ids = torch.tensor([3, 49, 0, 3], dtype=torch.int64)
     resid = torch.empty(4, cols, dtype=torch.bfloat16, device=DEV)
     y = torch.empty_like(resid)
-    call("q3_embed_rmsnorm", P(ids.to(DEV)), P(table.to(DEV)), P(resid), P(y), P(wd), 4, cols, 1e-6, S())
+    call("q3_embed_rmsnorm", P(dv(ids)), P(dv(table)), P(resid), P(y), P(wd), 4, cols, 1e-6, S())
     torch.cuda.synchronize()
     assert torch.equal(resid.cpu(), table[ids])
     assert_nearly_exact(y, oc.rms_norm(table[ids], w, 1e-6))
@@ -106,8 +129,8 @@ def test_qk_norm_rope_kv(B, T, start):
     ck = torch.zeros(B, Hkv, C, D, dtype=torch.bfloat16, device=DEV)
     cv = torch.zeros_like(ck)
     q_out = torch.empty(B * T, Hq, D, dtype=torch.bfloat16, device=DEV)
-    call("q3_qk_norm_rope_kv", P(qkv.to(DEV)), width, P(qw.to(DEV)), P(kw.to(DEV)), P(cos.to(DEV)),
-         P(sin.to(DEV)), None, start, P(q_out), P(ck), P(cv), B, T, Hq, Hkv, D, C, 1e-6, S())
+    call("q3_qk_norm_rope_kv", P(dv(qkv)), width, P(dv(qw)), P(dv(kw)), P(dv(cos)),
+         P(dv(sin)), None, start, P(q_out), P(ck), P(cv), B, T, Hq, Hkv, D, C, 1e-6, S())
     torch.cuda.synchronize()
     x = qkv.view(B, T, Hq + 2 * Hkv, D)
     c = cos[start:start + T].view(1, T, 1, D)
@@ -127,15 +150,23 @@ def test_qk_norm_rope_kv(B, T, start):
 # ------------------------------------------------------------ projections
 
 
-def ref_linear(x, w):
-    return (x.float() @ w.float().T)
+def check_projection(got, x, w, frac=0.03):
+    """``got`` vs the float64 dot products of the same BF16 operands.
 
-
-def check_projection(got, want_f32, frac=0.03):
-    want = want_f32.to(torch.bfloat16)
-    u = ulps(got.cpu(), want)
-    assert u.max() <= 1.0, f"max {u.max()} ulp"
-    assert (u > 0).mean() <= frac, f"{(u > 0).mean():.3f} differ"
+    Allowed error: one BF16 ulp of the exact value (the final rounding, plus
+    one rounding boundary crossed by summation error) and 2^-17 * sum|x*w|
+    (FP32 accumulation error of both orders, which dominates near zero).
+    Most elements must round exactly like the float64 sum.
+    """
+    x64 = x.float().numpy().astype(np.float64)
+    w64 = w.float().numpy().astype(np.float64)
+    exact = x64 @ w64.T
+    s_abs = np.abs(x64) @ np.abs(w64).T
+    g = got.cpu().float().numpy().astype(np.float64)
+    spacing = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 2.0 ** -126))) - 7)
+    err = np.abs(g - exact)
+    assert np.all(err <= spacing + 2.0 ** -17 * s_abs), f"max excess {(err - spacing - 2.0**-17 * s_abs).max():.3e}"
+    assert (g != oc.bf16_round(exact)).mean() <= frac, f"{(g != oc.bf16_round(exact)).mean():.3f} differ"
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
@@ -143,77 +174,81 @@ def check_projection(got, want_f32, frac=0.03):
 def test_gemv_plain_store(M, N, K):
     x, w = rnd((M, K), 1.0, M), rnd((N, K), 0.02, N + K)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
-    call("q3_gemv", _lib.X_PLAIN, P(x.to(DEV)), K, None, None, 0.0, None, P(w.to(DEV)), M, N, K,
+    call("q3_gemv", _lib.X_PLAIN, P(dv(x)), K, None, None, 0.0, None, P(dv(w)), M, N, K,
          _lib.EPI_STORE, P(y), N, None, None, S())
     torch.cuda.synchronize()
-    check_projection(y, ref_linear(x, w))
+    check_projection(y, x, w)
+
+
+def gemv(x_mode, x, ldx, w, M, N, K, epi, y, ldy, ids=None, norm_w=None, resid_out=None, pv=None, pi=None):
+    call("q3_gemv", x_mode, P(x), ldx, P(ids), P(norm_w), 1e-6, P(resid_out), P(w), M, N, K, epi, P(y), ldy,
+         P(pv), P(pi), S())
 
 
 @pytest.mark.parametrize("M", [1, 3, 8])
-def test_gemv_norm_resid_swiglu(M):
+def test_gemv_epilogues_and_norm_prologue(M):
+    """Each fused prologue/epilogue equals the unfused kernels it replaces, bit for bit."""
     K, N, I = 2560, 1024, 512
-    src = rnd((M, K), 1.0, 11)
-    g = (1 + rnd((K,), 0.2, 12).float()).to(torch.bfloat16)
-    w = rnd((N, K), 0.02, 13)
-    n_ref = oc.rms_norm(src, g, 1e-6)
-    # NORM prologue + STORE
-    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
-    srcd, gd, wd = src.to(DEV), g.to(DEV), w.to(DEV)
-    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wd), M, N, K, _lib.EPI_STORE, P(y), N,
-         None, None, S())
+    src = dv(rnd((M, K), 1.0, 11))
+    g = dv((1 + rnd((K,), 0.2, 12).float()).to(torch.bfloat16))
+    w = dv(rnd((N, K), 0.02, 13))
+    # NORM prologue == q3_rmsnorm then a plain GEMV (same reduction order).
+    n = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+    call("q3_rmsnorm", P(src), K, P(g), P(n), K, M, K, 1e-6, S())
+    y_ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    gemv(_lib.X_PLAIN, n, K, w, M, N, K, _lib.EPI_STORE, y_ref, N)
+    y = torch.empty_like(y_ref)
+    gemv(_lib.X_NORM, src, K, w, M, N, K, _lib.EPI_STORE, y, N, norm_w=g)
     torch.cuda.synchronize()
-    check_projection(y, ref_linear(n_ref, w), frac=0.05)
-    # RESID epilogue: y = bf16(res + bf16(acc)), in place.
+    assert torch.equal(y, y_ref)
+    assert_nearly_exact(n, oc.rms_norm(src.cpu(), g.cpu(), 1e-6))
+    # RESID epilogue == bf16(res + bf16(acc)), in place.
     res = rnd((M, N), 1.0, 14)
-    resd = res.to(DEV)
-    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wd), M, N, K, _lib.EPI_RESID, P(resd),
-         N, None, None, S())
+    resd = dv(res)
+    gemv(_lib.X_NORM, src, K, w, M, N, K, _lib.EPI_RESID, resd, N, norm_w=g)
     torch.cuda.synchronize()
-    want = res + ref_linear(n_ref, w).to(torch.bfloat16)
-    u = ulps(resd.cpu(), want)
-    assert u.max() <= 1.0 and (u > 0).mean() < 0.03
-    # SWIGLU epilogue on interleaved (gate, up) rows.
-    wg, wu = rnd((I, K), 0.02, 15), rnd((I, K), 0.02, 16)
-    wgu = torch.stack([wg, wu], 1).reshape(2 * I, K)
+    assert torch.equal(resd.cpu(), res + y.cpu())
+    # SWIGLU epilogue on interleaved (gate, up) rows == swiglu of the stored projections.
+    wgu = dv(torch.stack([rnd((I, K), 0.02, 15), rnd((I, K), 0.02, 16)], 1).reshape(2 * I, K))
+    gu = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=DEV)
+    gemv(_lib.X_NORM, src, K, wgu, M, 2 * I, K, _lib.EPI_STORE, gu, 2 * I, norm_w=g)
     act = torch.empty(M, I, dtype=torch.bfloat16, device=DEV)
-    call("q3_gemv", _lib.X_NORM, P(srcd), K, None, P(gd), 1e-6, None, P(wgu.to(DEV)), M, 2 * I, K,
-         _lib.EPI_SWIGLU, P(act), I, None, None, S())
+    gemv(_lib.X_NORM, src, K, wgu, M, 2 * I, K, _lib.EPI_SWIGLU, act, I, norm_w=g)
     torch.cuda.synchronize()
-    gate = ref_linear(n_ref, wg).to(torch.bfloat16)
-    up = ref_linear(n_ref, wu).to(torch.bfloat16)
-    want = oc.swiglu(gate, up)
-    u = ulps(act.cpu(), want)
-    assert u.max() <= 3 and (u > 0).mean() < 0.06
+    gu = gu.cpu()
+    assert_nearly_exact(act, oc.swiglu(gu[:, 0::2], gu[:, 1::2]), frac=5e-3)
 
 
 @pytest.mark.parametrize("M", [1, 4, 8])
 def test_gemv_embed_norm_and_argmax(M):
     V, K = 4096, 2560
     table = rnd((V, K), 0.02, 21)
-    g = (1 + rnd((K,), 0.2, 22).float()).to(torch.bfloat16)
+    g = dv((1 + rnd((K,), 0.2, 22).float()).to(torch.bfloat16))
     ids = torch.randint(0, V, (M,), generator=torch.Generator().manual_seed(M))
-    td, gd = table.to(DEV), g.to(DEV)
+    td, idd = dv(table), dv(ids)
     resid = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
     y = torch.empty(M, V, dtype=torch.bfloat16, device=DEV)
-    call("q3_gemv", _lib.X_EMBED_NORM, P(td), K, P(ids.to(DEV)), P(gd), 1e-6, P(resid), P(td), M, V, K,
-         _lib.EPI_STORE, P(y), V, None, None, S())
+    gemv(_lib.X_EMBED_NORM, td, K, td, M, V, K, _lib.EPI_STORE, y, V, ids=idd, norm_w=g, resid_out=resid)
+    n = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+    call("q3_rmsnorm", P(resid), K, P(g), P(n), K, M, K, 1e-6, S())
     torch.cuda.synchronize()
     assert torch.equal(resid.cpu(), table[ids])
-    n_ref = oc.rms_norm(table[ids], g, 1e-6)
-    check_projection(y, ref_linear(n_ref, table), frac=0.05)
+    check_projection(y, n.cpu(), table)
     # Fused argmax partials + finish == argmax of the stored logits (first index on ties).
     nparts = call("q3_gemv_partials", M, V, K)
     pv = torch.empty(nparts, M, dtype=torch.float32, device=DEV)
     pi = torch.empty(nparts, M, dtype=torch.int32, device=DEV)
     y2 = torch.empty_like(y)
-    call("q3_gemv", _lib.X_NORM, P(resid), K, None, P(gd), 1e-6, None, P(td), M, V, K, _lib.EPI_STORE_ARGMAX,
-         P(y2), V, P(pv), P(pi), S())
+    gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_STORE_ARGMAX, y2, V, norm_w=g, pv=pv, pi=pi)
     tok = torch.empty(M, dtype=torch.int64, device=DEV)
     pos = torch.tensor([5], dtype=torch.int64, device=DEV)
     call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), P(pos), S())
+    tok2 = torch.empty_like(tok)
+    gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi)
+    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok2), None, S())
     torch.cuda.synchronize()
     assert torch.equal(y2.cpu(), y.cpu())
-    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist()
+    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist() == tok2.cpu().tolist()
     assert pos.item() == 6
 
 
@@ -225,7 +260,7 @@ def test_argmax_rows_ties():
     x[2, [4999, 12, 13]] = 2.5
     tok = torch.empty(3, dtype=torch.int64, device=DEV)
     pos = torch.zeros(1, dtype=torch.int64, device=DEV)
-    call("q3_argmax_rows", P(x.to(DEV)), V, 3, V, P(tok), P(pos), S())
+    call("q3_argmax_rows", P(dv(x)), V, 3, V, P(tok), P(pos), S())
     torch.cuda.synchronize()
     assert tok.cpu().tolist() == [7, 0, 12] and pos.item() == 1
 
@@ -234,23 +269,20 @@ def test_argmax_rows_ties():
 @pytest.mark.parametrize("N,K", [(320, 1024), (1536, 320), (2560, 2560)])
 def test_gemm(M, N, K):
     x, w = rnd((M, K), 1.0, M + 1), rnd((N, K), 0.02, N + K + 1)
-    xd, wd = x.to(DEV), w.to(DEV)
+    xd, wd = dv(x), dv(w)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(y), N, S())
     torch.cuda.synchronize()
-    check_projection(y, ref_linear(x, w))
+    check_projection(y, x, w)
     res = rnd((M, N), 1.0, 5)
-    resd = res.to(DEV)
+    resd = dv(res)
     call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_RESID, P(resd), N, S())
     act = torch.empty(M, N // 2, dtype=torch.bfloat16, device=DEV)
     call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_SWIGLU, P(act), N // 2, S())
     torch.cuda.synchronize()
-    ref = ref_linear(x, w).to(torch.bfloat16)
-    u = ulps(resd.cpu(), res + ref)
-    assert u.max() <= 1.0 and (u > 0).mean() < 0.03
-    want = oc.swiglu(ref[:, 0::2], ref[:, 1::2])
-    u = ulps(act.cpu(), want)
-    assert u.max() <= 3 and (u > 0).mean() < 0.06
+    yc = y.cpu()
+    assert torch.equal(resd.cpu(), res + yc)
+    assert_nearly_exact(act, oc.swiglu(yc[:, 0::2], yc[:, 1::2]), frac=5e-3)
 
 
 # -------------------------------------------------------------- attention
@@ -279,7 +311,7 @@ def test_attn_decode(B, C, pos, splits):
     pml = torch.empty(B, Hq, splits, 2, dtype=torch.float32, device=DEV)
     out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
     posd = torch.tensor([pos], dtype=torch.int64, device=DEV)
-    call("q3_attn_decode", P(qkv.to(DEV)), width, P(qw.to(DEV)), P(kw.to(DEV)), P(cos.to(DEV)), P(sin.to(DEV)),
+    call("q3_attn_decode", P(dv(qkv)), width, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)),
          P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
     torch.cuda.synchronize()
@@ -311,7 +343,7 @@ def test_attn_prefill(B, T, start):
     ck = rnd((B, Hkv, C, D), 1.0, T + 1)
     cv = rnd((B, Hkv, C, D), 1.0, T + 2)
     out = torch.empty(B * T, Hq * D, dtype=torch.bfloat16, device=DEV)
-    call("q3_attn_prefill", P(q.to(DEV)), P(ck.to(DEV)), P(cv.to(DEV)), P(out), B, T, start, Hq, Hkv, C,
+    call("q3_attn_prefill", P(dv(q)), P(dv(ck)), P(dv(cv)), P(out), B, T, start, Hq, Hkv, C,
          D ** -0.5, S())
     torch.cuda.synchronize()
     qt = q.view(B, T, Hq, D).transpose(1, 2)
