@@ -59,7 +59,8 @@ def dominant_kernel_roofline(eng, reps: int = 20) -> dict:
     call("q3_graph_begin", s)
     for L in eng.layers:
         call("q3_gemv", _lib.X_NORM, eng.resid.data_ptr(), H, None, L["post_ln"].data_ptr(), eng.EPS, None,
-             L["gate_up"].data_ptr(), B, 2 * I, H, _lib.EPI_SWIGLU, eng.act.data_ptr(), I, None, None, s)
+             L["gate_up"].data_ptr(), B, 2 * I, H, _lib.EPI_SWIGLU, eng.act.data_ptr(), I, None, None,
+             None, None, None, s)
     ex = ctypes.c_void_p()
     call("q3_graph_end", s, ctypes.byref(ex))
     try:

@@ -48,15 +48,19 @@ const char *q3_error_string(int code);
 /* Decode projection for M <= 8 rows: y = epi(x' . W^T), x' per x_mode.
  * Replaces _linear (engine.py:431) fused with the input norm (engine.py:790,
  * fused.py:115 add_norm) and the residual / SwiGLU / argmax that follow it.
- * W is [N, K]; K % 8 == 0; x, W 16-byte aligned; ldx % 8 == 0.
- * EPI_SWIGLU writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
- * [q3_gemv_partials(M, N, K), M]; finish with q3_argmax_finish. */
+ * W is [N, K]; K % 8 == 0; x, W 16-byte aligned; ldx % 8 == 0.  Modes:
+ * X_EMBED_NORM with EPI_STORE; X_PLAIN with EPI_STORE or EPI_RESID; X_NORM
+ * with any epilogue.  EPI_SWIGLU writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
+ * [q3_gemv_partials(M, N, epi), M]; with tokens != NULL the last workgroup
+ * also reduces them into tokens[M] (int64), advances *pos when pos != NULL,
+ * and resets *counter (a device int, zero before the first call); otherwise
+ * finish with q3_argmax_finish. */
 int q3_gemv(int x_mode, const uint16_t *x, int ldx, const int64_t *ids,
             const uint16_t *norm_w, float eps, uint16_t *resid_out,
             const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, float *part_val, int *part_idx,
-            hipStream_t stream);
-int q3_gemv_partials(int M, int N, int K);
+            int64_t *tokens, int64_t *pos, int *counter, hipStream_t stream);
+int q3_gemv_partials(int M, int N, int epi);
 
 /* Dense projection for any M (MFMA, LDS-tiled): y = epi(x . W^T), epi in
  * {STORE, RESID, SWIGLU}.  Replaces F.linear / cuBLAS in prefill and at decode
@@ -97,12 +101,16 @@ int q3_qk_norm_rope_kv(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w
  * sequence), with the q/k RMSNorm + RoPE and the KV append of that token fused
  * in.  qkv [B, ld_qkv] (q | k | v); cache_k/v [B, Hkv, capacity, 128].
  * Writes per-split partials part_acc [B, Hq, splits, 128] (FP32, unnormalised)
- * and part_ml [B, Hq, splits, 2] (running max, sum).  Finish with
- * q3_attn_merge.  decode_attention_gqa / _split (fused.py:641-846). */
+ * and part_ml [B, Hq, splits, 2] (running max, sum).  With out != NULL the
+ * last workgroup of each (sequence, KV head) merges the splits into
+ * out [B, Hq*128] (BF16), using counter [B*Hkv] (device ints, zero before the
+ * first call, left zero); otherwise finish with q3_attn_merge.
+ * decode_attention_gqa / _split (fused.py:641-846). */
 int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w,
                    const uint16_t *k_norm_w, const uint16_t *cos_table,
                    const uint16_t *sin_table, const int64_t *pos,
                    uint16_t *cache_k, uint16_t *cache_v, float *part_acc, float *part_ml,
+                   uint16_t *out, int *counter,
                    int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                    hipStream_t stream);
 /* Log-sum-exp merge of the splits: out [B, Hq*128] BF16 (fused.py:793-823). */

@@ -27,14 +27,14 @@ _F = ctypes.c_float
 #: name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES = {
     "q3_error_string": [_I],
-    "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P],
+    "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
     "q3_gemv_partials": [_I, _I, _I],
     "q3_gemm": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P],
     "q3_rmsnorm": [_P, _I, _P, _P, _I, _I, _I, _F, _P],
     "q3_add_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "q3_embed_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "q3_qk_norm_rope_kv": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
-    "q3_attn_decode": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P],
+    "q3_attn_decode": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P],
     "q3_attn_merge": [_P, _P, _P, _I, _I, _I, _P],
     "q3_attn_splits": [_I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],

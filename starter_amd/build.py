@@ -59,11 +59,22 @@ def build_seed_lib() -> pathlib.Path:
 
 
 def build_hip_lib() -> pathlib.Path:
+    """Compile each .hip file to an object in parallel, then link one shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     OUT.mkdir(exist_ok=True)
+    objdir = OUT / "obj"
+    objdir.mkdir(exist_ok=True)
     target = OUT / "libq3.so"
     tmp = OUT / "libq3.so.tmp"
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    _run([hipcc, *HIPCC_FLAGS, *map(str, HIP_SOURCES), "-o", str(tmp)])
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs = [objdir / (src.stem + ".o") for src in HIP_SOURCES]
+    jobs = min(len(HIP_SOURCES), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda so: _run([hipcc, *compile_flags, "-c", str(so[0]), "-o", str(so[1])]),
+                      zip(HIP_SOURCES, objs)))
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, target)
     return target
 

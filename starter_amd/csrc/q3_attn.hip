@@ -115,12 +115,48 @@ struct DecodeArgs {
     bf16_t* cache_v;
     float* part_acc;
     float* part_ml;
+    bf16_t* out;   // fused merge target [B, Hq*D] (optional)
+    int* counter;  // [B*Hkv] arrival counters for the fused merge
     int Hq, Hkv, capacity, splits;
     float eps, scale;
 };
 
+// One 32-key block of K (as MFMA A operands) and V (raw rows) for a wave.
+struct KVBlock {
+    uint4 k[2][4];
+    uint4 v[8];
+};
+
+// Loads keys blk..blk+31 that lie below `limit` (rows past it read as zero).
+__device__ __forceinline__ void load_block(KVBlock& kb, const bf16_t* kbase, const bf16_t* vbase, int blk,
+                                           int limit, int g, int n) {
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+        const int key = blk + 16 * hb + n;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            kb.k[hb][kk] = key < limit ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + 32 * g + 8 * kk)
+                                       : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int key = blk + 4 * j + g;
+        kb.v[j] = key < limit ? *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + 8 * n)
+                              : make_uint4(0, 0, 0, 0);
+    }
+}
+
+// Split ranges are fixed by the capacity (not the live length), so a
+// workgroup knows its keys before it has read the position: the first block's
+// loads go out at entry, overlapping the position read and the q/k RoPE.
+__device__ __forceinline__ int split_len(int capacity, int splits) {
+    int per = (capacity + splits - 1) / splits;
+    return (per + BLK - 1) / BLK * BLK;
+}
+
 // grid (splits, Hkv, B); wave w of a workgroup takes blocks w, w+4, ... of the
-// split's key range; the four waves are merged through LDS at the end.
+// split's key range; the four waves merge through LDS, then the splits merge
+// in the last-arriving workgroup (or in attn_merge_kernel when out == NULL).
 __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -132,39 +168,42 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
     __shared__ __align__(16) bf16_t vs_all[4][BLK * D];
     __shared__ float mm[4][GROUP], ll[4][GROUP];
     __shared__ float macc[4][GROUP][D];
+    __shared__ int s_last;
 
-    const int pos = (int)*a.pos;
-    if (pos < 0 || pos >= a.capacity) {
-        // Out-of-range position (a caller bug): touch no cache memory, emit
-        // empty partials so the merge stays finite.
-        for (int e = tid; e < GROUP * D; e += THREADS) {
-            const int64_t p = ((int64_t)b * a.Hq + kvh * GROUP + e / D) * a.splits + split;
-            a.part_acc[p * D + e % D] = 0.f;
-            if (e % D == 0) { a.part_ml[2 * p] = -INFINITY; a.part_ml[2 * p + 1] = 0.f; }
-        }
-        return;
-    }
-    const int length = pos + 1;
-    int per = (length + a.splits - 1) / a.splits;
-    per = (per + BLK - 1) / BLK * BLK;
+    const int per = split_len(a.capacity, a.splits);
     const int begin = split * per;
-    const int end = min(begin + per, length);
-    const bool owner = begin <= pos && pos < end;
+    const int range_end = min(begin + per, a.capacity);
+    const bf16_t* kbase = a.cache_k + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
+    const bf16_t* vbase = a.cache_v + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
 
+    // Everything that does not depend on the position is requested first.
+    const int pos_raw = (int)*a.pos;
     const bf16_t* row = a.qkv + (int64_t)b * a.ld_qkv;
+    const bf16_t* qrow = row + (kvh * GROUP + w) * D;
+    const float q_lo = bf2f(qrow[lane]), q_hi = bf2f(qrow[lane + 64]);
+    const bf16_t* krow = row + a.Hq * D + kvh * D;
+    const bf16_t* vrow = row + (a.Hq + a.Hkv) * D + kvh * D;
+    KVBlock cur;
+    const int first = begin + w * BLK;
+    if (first < range_end) load_block(cur, kbase, vbase, first, range_end, g, n);
+
+    const bool bad_pos = pos_raw < 0 || pos_raw >= a.capacity;
+    const int pos = bad_pos ? 0 : pos_raw;
+    // Out-of-range position (a caller bug): touch no cache memory, process no keys.
+    const int end = bad_pos ? begin : min(range_end, pos + 1);
+    const bool owner = !bad_pos && begin <= pos && pos < end;
+
     const bf16_t* cosr = a.cos_t + (int64_t)pos * D;
     const bf16_t* sinr = a.sin_t + (int64_t)pos * D;
-    {
+    if (begin < end) {
         // Query head kvh*4 + w: RMSNorm + RoPE into LDS.
-        const bf16_t* q = row + (kvh * GROUP + w) * D;
         uint32_t lo, hi;
-        norm_rope_pair(bf2f(q[lane]), bf2f(q[lane + 64]), a.q_norm_w, cosr, sinr, a.eps, lane, lo, hi);
+        norm_rope_pair(q_lo, q_hi, a.q_norm_w, cosr, sinr, a.eps, lane, lo, hi);
         qs[w][lane] = (bf16_t)lo;
         qs[w][lane + 64] = (bf16_t)hi;
         if (owner && w == 0) {
             // This token's key: normalised, rotated, appended (fused.py:553-617).
-            const bf16_t* k = row + a.Hq * D + kvh * D;
-            norm_rope_pair(bf2f(k[lane]), bf2f(k[lane + 64]), a.k_norm_w, cosr, sinr, a.eps, lane, lo, hi);
+            norm_rope_pair(bf2f(krow[lane]), bf2f(krow[lane + 64]), a.k_norm_w, cosr, sinr, a.eps, lane, lo, hi);
             knew[lane] = (bf16_t)lo;
             knew[lane + 64] = (bf16_t)hi;
             bf16_t* dst = a.cache_k + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
@@ -172,8 +211,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
             dst[lane + 64] = (bf16_t)hi;
         }
         if (owner && w == 1) {
-            const bf16_t* v = row + (a.Hq + a.Hkv) * D + kvh * D;
-            const bf16_t v0 = v[lane], v1 = v[lane + 64];
+            const bf16_t v0 = vrow[lane], v1 = vrow[lane + 64];
             vnew[lane] = v0;
             vnew[lane + 64] = v1;
             bf16_t* dst = a.cache_v + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
@@ -183,78 +221,72 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
 
-    // Q^T operands, one per 32-wide slice of d: Q[n][32g + 8kk + t].
-    bf16x8_t qb[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * g + 8 * kk]);
-        qb[kk] = as_bf16x8(v);
-    }
-
-    const bf16_t* kbase = a.cache_k + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
-    const bf16_t* vbase = a.cache_v + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
-    bf16_t* vs = vs_all[w];
-
     float m = -INFINITY, l = 0.f;
     f32x4_t acc[8];
 #pragma unroll
     for (int dm = 0; dm < 8; ++dm) acc[dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int blk = begin + w * BLK; blk < end; blk += 4 * BLK) {
-        // K rows as the A operand: key blk + 16hb + n, d 32g .. 32g+31.
-        uint4 kr[2][4];
+    if (first < end) {
+        // Q^T operands, one per 32-wide slice of d: Q[n][32g + 8kk + t].
+        bf16x8_t qb[4];
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            const int key = blk + 16 * hb + n;
-            if (key < end) {
-                const uint4* src = (owner && key == pos)
-                    ? reinterpret_cast<const uint4*>(&knew[32 * g])
-                    : reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + 32 * g);
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) kr[hb][kk] = src[kk];
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) kr[hb][kk] = make_uint4(0, 0, 0, 0);
-            }
-        }
-        // V rows into this wave's LDS tile (row-contiguous global reads).
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = 4 * j + g, key = blk + r;
+        for (int kk = 0; kk < 4; ++kk) {
             uint4 v = make_uint4(0, 0, 0, 0);
-            if (key < end) {
-                v = (owner && key == pos) ? reinterpret_cast<const uint4*>(vnew)[n]
-                                          : *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + 8 * n);
+            if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * g + 8 * kk]);
+            qb[kk] = as_bf16x8(v);
+        }
+        bf16_t* vs = vs_all[w];
+        for (int blk = first; blk < end; blk += 4 * BLK) {
+            KVBlock nxt;
+            const int nb = blk + 4 * BLK;
+            if (nb < end) load_block(nxt, kbase, vbase, nb, end, g, n);
+            // The appended token replaces whatever the cache held at pos.
+            if (owner && blk <= pos && pos < blk + BLK) {
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb)
+                    if (blk + 16 * hb + n == pos)
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk)
+                            cur.k[hb][kk] = *reinterpret_cast<const uint4*>(&knew[32 * g + 8 * kk]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (blk + 4 * j + g == pos) cur.v[j] = reinterpret_cast<const uint4*>(vnew)[n];
             }
-            *reinterpret_cast<uint4*>(vs + r * D + v_chunk(r, n) * 8) = v;
-        }
-        f32x4_t s[2];
+            // V rows into this wave's LDS tile; rows at or past `end` are zero.
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 8; ++j) {
+                const int r = 4 * j + g;
+                const uint4 v = (blk + r < end) ? cur.v[j] : make_uint4(0, 0, 0, 0);
+                *reinterpret_cast<uint4*>(vs + r * D + v_chunk(r, n) * 8) = v;
+            }
+            f32x4_t s[2];
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[hb][kk]), qb[kk], s[hb], 0, 0, 0);
-        }
-        float s0[4], s1[4];
+            for (int hb = 0; hb < 2; ++hb) {
+                s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s0[i] = (blk + 4 * g + i < end) ? s[0][i] * a.scale : -INFINITY;
-            s1[i] = (blk + 16 + 4 * g + i < end) ? s[1][i] * a.scale : -INFINITY;
-        }
-        const float alpha = softmax_block(s0, s1, m, l);
-        const bf16x8_t pb = p_operand(s0, s1);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                for (int kk = 0; kk < 4; ++kk)
+                    s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.k[hb][kk]), qb[kk], s[hb], 0, 0, 0);
+            }
+            float s0[4], s1[4];
 #pragma unroll
-        for (int dm = 0; dm < 8; ++dm) {
-            acc[dm] *= alpha;
-            acc[dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand(vs, dm, n, g), pb, acc[dm], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                s0[i] = (blk + 4 * g + i < end) ? s[0][i] * a.scale : -INFINITY;
+                s1[i] = (blk + 16 + 4 * g + i < end) ? s[1][i] * a.scale : -INFINITY;
+            }
+            const float alpha = softmax_block(s0, s1, m, l);
+            const bf16x8_t pb = p_operand(s0, s1);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int dm = 0; dm < 8; ++dm) {
+                acc[dm] *= alpha;
+                acc[dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand(vs, dm, n, g), pb, acc[dm], 0, 0, 0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            cur = nxt;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
-    // Merge the four waves (each lane n < 4 holds head n: O^T[16dm + 4g + i][n]).
+    // Merge the four waves (lane n < 4 holds head n: O^T[16dm + 4g + i][n]).
     if (n < GROUP) {
         if (g == 0) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
@@ -286,27 +318,89 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
             a.part_ml[2 * p + 1] = sl;
         }
     }
+    if (a.out == nullptr) return;
+
+    // Log-sum-exp merge of the splits by the last workgroup of this (b, kvh)
+    // (reference fused.py:793-823).  The others exit; nothing waits.
+    __syncthreads();
+    int* cnt = a.counter + b * a.Hkv + kvh;
+    if (tid == 0) {
+        __threadfence();
+        const int prev = atomicAdd(cnt, 1);
+        s_last = (prev == a.splits - 1);
+        __threadfence();
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int e = tid; e < GROUP * D; e += THREADS) {
+        const int h = e / D, d = e % D;
+        const int qh = kvh * GROUP + h;
+        const int64_t base = ((int64_t)b * a.Hq + qh) * a.splits;
+        float M = -INFINITY;
+        for (int sp = 0; sp < a.splits; ++sp) {
+            const float* ml = a.part_ml + 2 * (base + sp);
+            if (__builtin_nontemporal_load(ml + 1) > 0.f) M = fmaxf(M, __builtin_nontemporal_load(ml));
+        }
+        float sacc = 0.f, tot = 0.f;
+        for (int sp = 0; sp < a.splits; ++sp) {
+            const float* ml = a.part_ml + 2 * (base + sp);
+            const float ls = __builtin_nontemporal_load(ml + 1);
+            if (ls > 0.f) {
+                const float wt = expf(__builtin_nontemporal_load(ml) - M);
+                sacc += __builtin_nontemporal_load(a.part_acc + (base + sp) * D + d) * wt;
+                tot += ls * wt;
+            }
+        }
+        a.out[((int64_t)b * a.Hq + qh) * D + d] = (bf16_t)f2bf(tot > 0.f ? sacc / tot : 0.f);
+    }
+    if (tid == 0) *cnt = 0;  // ready for the next launch
 }
 
-// grid (Hq, B), 128 threads: log-sum-exp merge of the split partials
-// (reference fused.py:793-823).
+// grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
+// partials (reference fused.py:793-823).  Latency-shaped: the (max, sum)
+// pairs go through LDS in one cooperative load, the accumulators are read 16
+// splits at a time with every load issued before any arithmetic, and each
+// chunk is folded into a running (max, sum, acc) like the decode softmax.
 __global__ __launch_bounds__(D) void attn_merge_kernel(const float* part_acc, const float* part_ml,
                                                        bf16_t* out, int Hq, int splits) {
+    constexpr int CH = 16;
+    __shared__ float sml[2 * 256];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int64_t base = ((int64_t)b * Hq + h) * splits;
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s)
-        if (part_ml[2 * (base + s) + 1] > 0.f) M = fmaxf(M, part_ml[2 * (base + s)]);
-    float acc = 0.f, tot = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float ls = part_ml[2 * (base + s) + 1];
-        if (ls > 0.f) {
-            const float wt = expf(part_ml[2 * (base + s)] - M);
-            acc += part_acc[(base + s) * D + d] * wt;
-            tot += ls * wt;
+    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < splits; s0 += 256) {
+        const int n = min(256, splits - s0);
+        __syncthreads();
+        for (int e = d; e < 2 * n; e += D) sml[e] = part_ml[2 * (base + s0) + e];
+        __syncthreads();
+        for (int c0 = 0; c0 < n; c0 += CH) {
+            float av[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                av[j] = (c0 + j < n) ? part_acc[(base + s0 + c0 + j) * D + d] : 0.f;
+            float cm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                if (c0 + j < n && sml[2 * (c0 + j) + 1] > 0.f) cm = fmaxf(cm, sml[2 * (c0 + j)]);
+            if (cm == -INFINITY) continue;
+            const float m_new = fmaxf(m_run, cm);
+            const float scale = expf(m_run - m_new);
+            acc *= scale;
+            l_run *= scale;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const float ls = (c0 + j < n) ? sml[2 * (c0 + j) + 1] : 0.f;
+                if (ls > 0.f) {
+                    const float wt = expf(sml[2 * (c0 + j)] - m_new);
+                    acc += av[j] * wt;
+                    l_run += ls * wt;
+                }
+            }
+            m_run = m_new;
         }
     }
-    out[((int64_t)b * Hq + h) * D + d] = (bf16_t)f2bf(tot > 0.f ? acc / tot : 0.f);
+    out[((int64_t)b * Hq + h) * D + d] = (bf16_t)f2bf(l_run > 0.f ? acc / l_run : 0.f);
 }
 
 // ----------------------------------------------------------------- prefill
@@ -438,13 +532,15 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const bf16_t* q_nor
                               const bf16_t* k_norm_w, const bf16_t* cos_table,
                               const bf16_t* sin_table, const int64_t* pos,
                               bf16_t* cache_k, bf16_t* cache_v, float* part_acc, float* part_ml,
+                              bf16_t* out, int* counter,
                               int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                               hipStream_t stream) {
     if (B < 1 || Hkv < 1 || Hq != GROUP * Hkv || capacity < 1 || splits < 1 || ld_qkv < (Hq + 2 * Hkv) * D)
         return (int)hipErrorInvalidValue;
-    if (!qkv || !pos || !cache_k || !cache_v || !part_acc || !part_ml) return (int)hipErrorInvalidValue;
+    if (!qkv || !pos || !cache_k || !cache_v || !part_acc || !part_ml || (out && !counter))
+        return (int)hipErrorInvalidValue;
     DecodeArgs a{qkv, ld_qkv, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
-                 part_acc, part_ml, Hq, Hkv, capacity, splits, eps, scale};
+                 part_acc, part_ml, out, counter, Hq, Hkv, capacity, splits, eps, scale};
     hipLaunchKernelGGL(attn_decode_kernel, dim3(splits, Hkv, B), dim3(THREADS), 0, stream, a);
     Q3_CHECK_LAUNCH();
 }

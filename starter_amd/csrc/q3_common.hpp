@@ -38,10 +38,20 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo 
 
 // --------------------------------------------------------------- reductions
 
+// Sum over the 64 lanes, returned to every lane.  DPP sums each 16-lane row
+// (quad swaps, then rotations by 4 and 8 within the row); the four row sums
+// are read from lanes 0/16/32/48 and added in a fixed order.
+#define Q3_DPP(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false))
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, Q3_WAVE);
-    return v;
+    v += Q3_DPP(v, 0xb1);   // quad_perm [1,0,3,2]
+    v += Q3_DPP(v, 0x4e);   // quad_perm [2,3,0,1]
+    v += Q3_DPP(v, 0x124);  // row_ror:4
+    v += Q3_DPP(v, 0x128);  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -2,13 +2,17 @@
 //
 // Reference: engine/engine.py:431-450 (_linear) -> engine/kernels/fused.py:315-550
 // (skinny_linear / _t / _split).  At batch 1-8 a projection is pure weight
-// streaming, so the kernel is shaped around HBM: each wave owns R whole weight
-// rows and its 64 lanes sweep K with 16-byte loads (a 1 KiB contiguous run per
-// wave per row per step), with enough waves per CU that ~64 KiB is in flight.
-// The 8-element products go through v_dot2_f32_bf16 (exact BF16 products, FP32
-// accumulation), and the 64 lane partials of each (row, batch) are combined by
-// a butterfly.  The summation order differs from cuBLAS/oneDNN, which is the
-// reordering the reference accepts (AGENTS.md "Numerics").
+// streaming, so the kernel is shaped around HBM:
+//   * each wave owns R whole weight rows; lane l reads 16-byte chunks
+//     l, l+64, l+128, ... of each row, so a wave's load is one contiguous
+//     1 KiB run per row;
+//   * for the model's K (512*KU, KU compile-time) every weight load of the
+//     wave is issued up front, before the prologue and before any arithmetic,
+//     so a whole matrix is in flight across the CUs at once;
+//   * products go through v_dot2_f32_bf16 (exact BF16 products, FP32
+//     accumulation); each (row, batch) sum is reduced across the wave with DPP.
+// The summation order differs from cuBLAS/oneDNN: the reordering the
+// reference accepts (AGENTS.md "Numerics").
 //
 // Fused around it:
 //   prologue  X_NORM       x = RMSNorm(src) computed per workgroup into LDS
@@ -19,8 +23,10 @@
 //                          (fused.py:135-138);
 //             EPI_SWIGLU   weight rows interleaved (gate_j, up_j);
 //                          out[j] = bf16(bf16(silu(g)) * u) (fused.py:107-111);
-//             EPI_ARGMAX   per-workgroup (max bf16 logit, lowest index) partials
-//                          for the fused LM-head argmax (engine.py:833).
+//             EPI_ARGMAX   per-workgroup (max bf16 logit, lowest index) partials;
+//                          with tokens != NULL the last workgroup to finish
+//                          (device-scope counter) reduces them, writes the
+//                          greedy tokens and advances *pos (engine.py:833-838).
 #include "q3_common.hpp"
 #include "q3.h"
 
@@ -28,9 +34,10 @@ namespace {
 
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / Q3_WAVE;
+constexpr int LDS_X_LIMIT = 60 * 1024;
 
 struct GemvArgs {
-    const bf16_t* x;      // X_PLAIN: input rows; X_NORM: rows to normalise
+    const bf16_t* x;      // X_PLAIN: input rows; X_NORM: rows to normalise; X_EMBED_NORM: table
     int ldx;
     const int64_t* ids;   // X_EMBED_NORM: token ids [M]
     const bf16_t* norm_w; // X_NORM / X_EMBED_NORM gain [K]
@@ -38,80 +45,211 @@ struct GemvArgs {
     bf16_t* resid_out;    // X_EMBED_NORM: embedding rows copied here [M, K]
     const bf16_t* w;      // weights [N, K]
     int M, N, K;
-    bf16_t* y;            // output (EPI_STORE / EPI_RESID / EPI_SWIGLU)
+    bf16_t* y;            // output (EPI_STORE / EPI_RESID / EPI_SWIGLU / EPI_STORE_ARGMAX)
     int ldy;
     float* part_val;      // EPI_ARGMAX: [gridDim.x, M]
     int* part_idx;
+    int64_t* tokens;      // fused argmax finish (optional)
+    int64_t* pos;
+    int* counter;
 };
 
-// Normalise M rows of K into LDS (BF16), one workgroup-wide pass per row set.
-template <int M, int XMODE>
-__device__ void norm_prologue(const GemvArgs& a, bf16_t* xs) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    __shared__ float red[GEMV_WAVES][M];
-    float ss[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) ss[m] = 0.f;
-    const int chunks = a.K >> 3;
-    for (int c = tid; c < chunks; c += GEMV_THREADS) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const bf16_t* src;
-            if (XMODE == Q3_X_EMBED_NORM) src = a.x + a.ids[m] * (int64_t)a.K;
-            else src = a.x + (int64_t)m * a.ldx;
-            uint4 v = *reinterpret_cast<const uint4*>(src + c * 8);
-            *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) = v;
-            if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
-                *reinterpret_cast<uint4*>(a.resid_out + (int64_t)m * a.K + c * 8) = v;
-            float s = ss[m];
-            s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
-            s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
-            s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
-            s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
-            ss[m] = s;
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float s = wave_sum(ss[m]);
-        if (lane == 0) red[wave][m] = s;
-    }
-    __syncthreads();
-    float inv[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float s = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
-        inv[m] = inv_rms(s, a.K, a.eps);
-    }
-    for (int c = tid; c < chunks; c += GEMV_THREADS) {
-        uint4 g = *reinterpret_cast<const uint4*>(a.norm_w + c * 8);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            uint4* p = reinterpret_cast<uint4*>(xs + m * a.K + c * 8);
-            uint4 v = *p;
-            float im = inv[m];
-            v.x = pack2(norm_elem(bflo(v.x), im, bflo(g.x)), norm_elem(bfhi(v.x), im, bfhi(g.x)));
-            v.y = pack2(norm_elem(bflo(v.y), im, bflo(g.y)), norm_elem(bfhi(v.y), im, bfhi(g.y)));
-            v.z = pack2(norm_elem(bflo(v.z), im, bflo(g.z)), norm_elem(bfhi(v.z), im, bfhi(g.z)));
-            v.w = pack2(norm_elem(bflo(v.w), im, bflo(g.w)), norm_elem(bfhi(v.w), im, bfhi(g.w)));
-            *p = v;
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
 }
 
-template <int M, int R, int XMODE, int EPI>
+// Stage the M input rows into LDS (BF16), normalised for the NORM modes.
+template <int M, int XMODE>
+__device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int chunks = a.K >> 3;
+    if constexpr (XMODE == Q3_X_PLAIN) {
+        for (int c = tid; c < chunks; c += GEMV_THREADS)
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+                *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) =
+                    *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + c * 8);
+        __syncthreads();
+        return;
+    } else {
+        __shared__ float red[GEMV_WAVES][M];
+        float ss[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) ss[m] = 0.f;
+        for (int c = tid; c < chunks; c += GEMV_THREADS) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const bf16_t* src;
+                if (XMODE == Q3_X_EMBED_NORM) src = a.x + a.ids[m] * (int64_t)a.K;
+                else src = a.x + (int64_t)m * a.ldx;
+                uint4 v = *reinterpret_cast<const uint4*>(src + c * 8);
+                *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) = v;
+                if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
+                    *reinterpret_cast<uint4*>(a.resid_out + (int64_t)m * a.K + c * 8) = v;
+                float s = ss[m];
+                s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
+                s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
+                s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
+                s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
+                ss[m] = s;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = wave_sum(ss[m]);
+            if (lane == 0) red[wave][m] = s;
+        }
+        __syncthreads();
+        float inv[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+            inv[m] = inv_rms(s, a.K, a.eps);
+        }
+        for (int c = tid; c < chunks; c += GEMV_THREADS) {
+            uint4 g = *reinterpret_cast<const uint4*>(a.norm_w + c * 8);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                uint4* p = reinterpret_cast<uint4*>(xs + m * a.K + c * 8);
+                uint4 v = *p;
+                float im = inv[m];
+                v.x = pack2(norm_elem(bflo(v.x), im, bflo(g.x)), norm_elem(bfhi(v.x), im, bfhi(g.x)));
+                v.y = pack2(norm_elem(bflo(v.y), im, bflo(g.y)), norm_elem(bfhi(v.y), im, bfhi(g.y)));
+                v.z = pack2(norm_elem(bflo(v.z), im, bflo(g.z)), norm_elem(bfhi(v.z), im, bfhi(g.z)));
+                v.w = pack2(norm_elem(bflo(v.w), im, bflo(g.w)), norm_elem(bfhi(v.w), im, bfhi(g.w)));
+                *p = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// x chunk (16 bytes) of batch row m at element k, from LDS or global.
+template <bool XLDS>
+__device__ __forceinline__ uint4 xchunk(const GemvArgs& a, const bf16_t* xs, int m, int k) {
+    if constexpr (XLDS) return *reinterpret_cast<const uint4*>(xs + m * a.K + k);
+    else return *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k);
+}
+
+// Epilogue for the non-argmax modes: lane r*M+m owns output (row0+r, m).
+template <int M, int R, int EPI>
+__device__ __forceinline__ void store_outputs(const GemvArgs& a, const float (&acc)[R][M], int row0, int lane) {
+    if (lane >= R * M) return;
+    const int r = lane / M, m = lane % M;
+    float v = 0.f, vpair = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            if (rr == r && mm == m) v = acc[rr][mm];
+            if (rr == (r | 1) && mm == m) vpair = acc[rr][mm];
+        }
+    if constexpr (EPI == Q3_EPI_STORE || EPI == Q3_EPI_STORE_ARGMAX) {
+        a.y[(int64_t)m * a.ldy + row0 + r] = (bf16_t)f2bf(v);
+    } else if constexpr (EPI == Q3_EPI_RESID) {
+        bf16_t* p = a.y + (int64_t)m * a.ldy + row0 + r;
+        *p = (bf16_t)f2bf(bf2f(*p) + rbf(v));
+    } else if constexpr (EPI == Q3_EPI_SWIGLU) {
+        if ((r & 1) == 0) {
+            const float g = rbf(v), u = rbf(vpair);
+            a.y[(int64_t)m * a.ldy + ((row0 + r) >> 1)] = (bf16_t)f2bf(silu_bf16(g) * u);
+        }
+    }
+}
+
+// Argmax partials of this workgroup, and the fused finish in the last one.
+template <int M, int R>
+__device__ void argmax_epilogue(const GemvArgs& a, const float (&acc)[R][M], int row0, bool active,
+                                int lane, int wave) {
+    __shared__ float bval[GEMV_WAVES][M];
+    __shared__ int bidx[GEMV_WAVES][M];
+    __shared__ int s_last;
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float best = -INFINITY;
+            int bi = 0x7fffffff;
+            if (active) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float v = rbf(acc[r][m]);
+                    if (v > best) { best = v; bi = row0 + r; }
+                }
+            }
+            bval[wave][m] = best;
+            bidx[wave][m] = bi;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < M) {
+        const int m = threadIdx.x;
+        float best = bval[0][m];
+        int bi = bidx[0][m];
+#pragma unroll
+        for (int w = 1; w < GEMV_WAVES; ++w)
+            if (better(bval[w][m], bidx[w][m], best, bi)) { best = bval[w][m]; bi = bidx[w][m]; }
+        a.part_val[blockIdx.x * M + m] = best;
+        a.part_idx[blockIdx.x * M + m] = bi;
+    }
+    if (a.tokens == nullptr) return;
+    // The last workgroup to arrive reduces every partial; the others just exit
+    // (nothing waits on anything, so no workgroup can stall the grid).
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const int prev = atomicAdd(a.counter, 1);
+        s_last = (prev == (int)gridDim.x - 1);
+        __threadfence();
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    const int nparts = gridDim.x;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int p = threadIdx.x; p < nparts; p += GEMV_THREADS) {
+            const float v = __builtin_nontemporal_load(a.part_val + p * M + m);
+            const int i = __builtin_nontemporal_load(a.part_idx + p * M + m);
+            if (better(v, i, bv, bi)) { bv = v; bi = i; }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float v = __shfl_xor(bv, o, Q3_WAVE);
+            const int i = __shfl_xor(bi, o, Q3_WAVE);
+            if (better(v, i, bv, bi)) { bv = v; bi = i; }
+        }
+        __syncthreads();
+        if (lane == 0) { bval[wave][m] = bv; bidx[wave][m] = bi; }
+    }
+    __syncthreads();
+    if (threadIdx.x < M) {
+        const int m = threadIdx.x;
+        float bv = bval[0][m];
+        int bi = bidx[0][m];
+#pragma unroll
+        for (int w = 1; w < GEMV_WAVES; ++w)
+            if (better(bval[w][m], bidx[w][m], bv, bi)) { bv = bval[w][m]; bi = bidx[w][m]; }
+        a.tokens[m] = bi;
+    }
+    if (threadIdx.x == 0) {
+        if (a.pos) *a.pos += 1;
+        *a.counter = 0;  // ready for the next launch (kernel boundaries order it)
+    }
+}
+
+// KU > 0: K == 512*KU, all weight loads issued up front.  KU == 0: any K % 8 == 0.
+template <int M, int R, int KU, int XMODE, bool XLDS, int EPI>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     bf16_t* xs = reinterpret_cast<bf16_t*>(smem);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-
-    if constexpr (XMODE != Q3_X_PLAIN) norm_prologue<M, XMODE>(a, xs);
-
     const int row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
     const bool active = row0 < a.N;
     const int K = a.K;
+    const bf16_t* wrow = a.w + (int64_t)row0 * K + lane * 8;
 
     float acc[R][M];
 #pragma unroll
@@ -119,45 +257,38 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
 
-    if (active) {
-        const bf16_t* wrow = a.w + (int64_t)row0 * K;
-        // Two K-steps per iteration so each wave keeps 2R 16-byte loads in flight.
-        int k = lane * 8;
-        for (; k + 512 < K; k += 1024) {
-            uint4 wv0[R], wv1[R];
+    if constexpr (KU > 0) {
+        uint4 wv[R][KU];
+        if (active) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                wv0[r] = load_nt((wrow + (int64_t)r * K + k));
-                wv1[r] = load_nt((wrow + (int64_t)r * K + k + 512));
-            }
+            for (int u = 0; u < KU; ++u)
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                uint4 x0, x1;
-                if constexpr (XMODE == Q3_X_PLAIN) {
-                    x0 = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k);
-                    x1 = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k + 512);
-                } else {
-                    x0 = *reinterpret_cast<const uint4*>(xs + m * K + k);
-                    x1 = *reinterpret_cast<const uint4*>(xs + m * K + k + 512);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv1[r], x1, dot8(wv0[r], x0, acc[r][m]));
-            }
+                for (int r = 0; r < R; ++r) wv[r][u] = load_nt(wrow + (int64_t)r * K + u * 512);
         }
-        if (k < K) {
-            uint4 wv0[R];
+        if constexpr (XLDS) stage_x<M, XMODE>(a, xs);
+        if (active) {
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                wv0[r] = load_nt((wrow + (int64_t)r * K + k));
+            for (int u = 0; u < KU; ++u)
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                uint4 x0;
-                if constexpr (XMODE == Q3_X_PLAIN)
-                    x0 = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k);
-                else
-                    x0 = *reinterpret_cast<const uint4*>(xs + m * K + k);
+                for (int m = 0; m < M; ++m) {
+                    const uint4 xv = xchunk<XLDS>(a, xs, m, lane * 8 + u * 512);
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv0[r], x0, acc[r][m]);
+                    for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv[r][u], xv, acc[r][m]);
+                }
+        }
+    } else {
+        if constexpr (XLDS) stage_x<M, XMODE>(a, xs);
+        if (active) {
+            for (int k = lane * 8; k < K; k += 512) {
+                uint4 wv[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) wv[r] = load_nt(wrow + (int64_t)r * K + (k - lane * 8));
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint4 xv = xchunk<XLDS>(a, xs, m, k);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv[r], xv, acc[r][m]);
+                }
             }
         }
     }
@@ -167,97 +298,62 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
         for (int m = 0; m < M; ++m) acc[r][m] = wave_sum(acc[r][m]);
 
     if constexpr (EPI == Q3_EPI_ARGMAX || EPI == Q3_EPI_STORE_ARGMAX) {
-        __shared__ float bval[GEMV_WAVES][M];
-        __shared__ int bidx[GEMV_WAVES][M];
-        if (lane == 0) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                float best = -INFINITY;
-                int bi = 0x7fffffff;
-                if (active) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float v = rbf(acc[r][m]);
-                        if (v > best) { best = v; bi = row0 + r; }
-                    }
-                }
-                bval[wave][m] = best;
-                bidx[wave][m] = bi;
-            }
-        }
-        if constexpr (EPI == Q3_EPI_STORE_ARGMAX) {
-            if (active && lane < R * M) {
-                const int r = lane / M, m = lane % M;
-                float v = 0.f;
-#pragma unroll
-                for (int rr = 0; rr < R; ++rr)
-#pragma unroll
-                    for (int mm = 0; mm < M; ++mm)
-                        if (rr == r && mm == m) v = acc[rr][mm];
-                a.y[(int64_t)m * a.ldy + row0 + r] = (bf16_t)f2bf(v);
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x < M) {
-            const int m = threadIdx.x;
-            float best = bval[0][m];
-            int bi = bidx[0][m];
-#pragma unroll
-            for (int w = 1; w < GEMV_WAVES; ++w) {
-                float v = bval[w][m];
-                int i = bidx[w][m];
-                if (v > best || (v == best && i < bi)) { best = v; bi = i; }
-            }
-            a.part_val[blockIdx.x * M + m] = best;
-            a.part_idx[blockIdx.x * M + m] = bi;
-        }
-        return;
+        if constexpr (EPI == Q3_EPI_STORE_ARGMAX)
+            if (active) store_outputs<M, R, EPI>(a, acc, row0, lane);
+        argmax_epilogue<M, R>(a, acc, row0, active, lane, wave);
     } else {
-        if (!active || lane >= R * M) return;
-        const int r = lane / M, m = lane % M;
-        // Select this lane's (r, m) value with compile-time indices only.
-        float v = 0.f, vpair = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr)
-#pragma unroll
-            for (int mm = 0; mm < M; ++mm) {
-                if (rr == r && mm == m) v = acc[rr][mm];
-                if (rr == (r | 1) && mm == m) vpair = acc[rr][mm];
-            }
-        if constexpr (EPI == Q3_EPI_STORE) {
-            a.y[(int64_t)m * a.ldy + row0 + r] = (bf16_t)f2bf(v);
-        } else if constexpr (EPI == Q3_EPI_RESID) {
-            bf16_t* p = a.y + (int64_t)m * a.ldy + row0 + r;
-            *p = (bf16_t)f2bf(bf2f(*p) + rbf(v));
-        } else if constexpr (EPI == Q3_EPI_SWIGLU) {
-            if ((r & 1) == 0) {
-                const float g = rbf(v), u = rbf(vpair);
-                a.y[(int64_t)m * a.ldy + ((row0 + r) >> 1)] = (bf16_t)f2bf(silu_bf16(g) * u);
-            }
-        }
+        if (active) store_outputs<M, R, EPI>(a, acc, row0, lane);
     }
 }
 
-template <int M, int R, int XMODE, int EPI>
+// Rows per wave.  Projections: one row per wave, so the N rows spread over N
+// waves and every CU streams.  SwiGLU needs the (gate, up) pair.  The LM-head
+// argmax (N ~ 152k) has waves to spare and takes four rows (two at M > 4),
+// which keeps its partials few.
+constexpr int rows_per_wave(int M, int epi) {
+    return epi == Q3_EPI_SWIGLU ? 2
+         : (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) ? (M > 4 ? 2 : 4)
+         : 1;
+}
+
+// The (input mode, epilogue) pairs the decode step and the prompt pass use.
+constexpr bool combo_used(int xmode, int epi) {
+    return xmode == Q3_X_EMBED_NORM ? epi == Q3_EPI_STORE
+         : xmode == Q3_X_PLAIN ? (epi == Q3_EPI_STORE || epi == Q3_EPI_RESID)
+         : true;
+}
+
+template <int M, int KU, int XMODE, bool XLDS, int EPI>
 int launch_one(const GemvArgs& a, hipStream_t stream) {
-    const int waves = a.N / R;
-    const int blocks = (waves + GEMV_WAVES - 1) / GEMV_WAVES;
-    const size_t shmem = (XMODE == Q3_X_PLAIN) ? 0 : (size_t)M * a.K * sizeof(bf16_t);
-    hipLaunchKernelGGL((gemv_dot2_kernel<M, R, XMODE, EPI>), dim3(blocks), dim3(GEMV_THREADS),
+    constexpr int R = rows_per_wave(M, EPI);
+    if (a.N % R != 0) return -1;
+    const int blocks = (a.N / R + GEMV_WAVES - 1) / GEMV_WAVES;
+    const size_t shmem = XLDS ? (size_t)M * a.K * sizeof(bf16_t) : 0;
+    hipLaunchKernelGGL((gemv_dot2_kernel<M, R, KU, XMODE, XLDS, EPI>), dim3(blocks), dim3(GEMV_THREADS),
                        shmem, stream, a);
     Q3_CHECK_LAUNCH();
 }
 
-// Rows per wave: enough 16-byte loads in flight per wave for short K,
-// fewer accumulators for long K or many batch rows.
-int rows_per_wave(int M, int K) { return (K >= 8192 || M > 4) ? 2 : 4; }
+template <int M, int XMODE, bool XLDS, int EPI>
+int launch_ku(const GemvArgs& a, hipStream_t stream) {
+    switch (a.K) {
+        case 2560: return launch_one<M, 5, XMODE, XLDS, EPI>(a, stream);
+        case 4096: return launch_one<M, 8, XMODE, XLDS, EPI>(a, stream);
+        case 9728: return launch_one<M, 19, XMODE, XLDS, EPI>(a, stream);
+    }
+    return launch_one<M, 0, XMODE, XLDS, EPI>(a, stream);
+}
 
 template <int M, int XMODE, int EPI>
 int launch_rows(const GemvArgs& a, hipStream_t stream) {
-    const int R = rows_per_wave(M, a.K);
-    if (a.N % R != 0) return -1;
-    if (R == 2) return launch_one<M, 2, XMODE, EPI>(a, stream);
-    return launch_one<M, 4, XMODE, EPI>(a, stream);
+    if constexpr (!combo_used(XMODE, EPI)) {
+        return -1;
+    } else if constexpr (XMODE != Q3_X_PLAIN) {
+        return launch_ku<M, XMODE, true, EPI>(a, stream);
+    } else {
+        if ((size_t)M * a.K * 2 <= LDS_X_LIMIT) return launch_ku<M, XMODE, true, EPI>(a, stream);
+        return launch_ku<M, XMODE, false, EPI>(a, stream);
+    }
 }
 
 template <int XMODE, int EPI>
@@ -289,9 +385,9 @@ int dispatch_epi(int epi, const GemvArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-extern "C" int q3_gemv_partials(int M, int N, int K) {
+extern "C" int q3_gemv_partials(int M, int N, int epi) {
     // Workgroups (= argmax partial rows) the GEMV launches for N weight rows.
-    const int R = rows_per_wave(M, K);
+    const int R = rows_per_wave(M, epi);
     return (N / R + GEMV_WAVES - 1) / GEMV_WAVES;
 }
 
@@ -299,19 +395,22 @@ extern "C" int q3_gemv(int x_mode, const bf16_t* x, int ldx, const int64_t* ids,
                        const bf16_t* norm_w, float eps, bf16_t* resid_out,
                        const bf16_t* w, int M, int N, int K,
                        int epi, bf16_t* y, int ldy, float* part_val, int* part_idx,
-                       hipStream_t stream) {
+                       int64_t* tokens, int64_t* pos, int* counter, hipStream_t stream) {
     if (M < 1 || M > Q3_GEMV_MAX_M || N < 1 || K < 8 || (K % 8) != 0) return (int)hipErrorInvalidValue;
-    // The normalised rows live in LDS (M*K BF16, within the 64 KiB default).
-    if (x_mode != Q3_X_PLAIN && (K > Q3_GEMV_MAX_NORM_K || M * K * 2 > 60 * 1024)) return (int)hipErrorInvalidValue;
-    if (epi == Q3_EPI_SWIGLU && (N % 2) != 0) return (int)hipErrorInvalidValue;
-    if ((epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) && (!part_val || !part_idx))
+    // Staged rows live in LDS (M*K BF16, within the 64 KiB default).
+    if (x_mode != Q3_X_PLAIN && (K > Q3_GEMV_MAX_NORM_K || (size_t)M * K * 2 > LDS_X_LIMIT))
         return (int)hipErrorInvalidValue;
+    if (epi == Q3_EPI_SWIGLU && (N % 2) != 0) return (int)hipErrorInvalidValue;
+    const bool argmax = epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX;
+    if (argmax && (!part_val || !part_idx)) return (int)hipErrorInvalidValue;
+    if (argmax && tokens && !counter) return (int)hipErrorInvalidValue;
     if (epi != Q3_EPI_ARGMAX && !y) return (int)hipErrorInvalidValue;
     if (x_mode == Q3_X_EMBED_NORM && (!ids || !resid_out)) return (int)hipErrorInvalidValue;
     if (x_mode != Q3_X_PLAIN && !norm_w) return (int)hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return (int)hipErrorInvalidValue;
     if (x_mode == Q3_X_PLAIN && (ldx % 8) != 0) return (int)hipErrorInvalidValue;
-    GemvArgs a{x, ldx, ids, norm_w, eps, resid_out, w, M, N, K, y, ldy, part_val, part_idx};
+    GemvArgs a{x, ldx, ids, norm_w, eps, resid_out, w, M, N, K, y, ldy, part_val, part_idx,
+               argmax ? tokens : nullptr, pos, counter};
     int rc = -1;
     switch (x_mode) {
         case Q3_X_PLAIN: rc = dispatch_epi<Q3_X_PLAIN>(epi, a, stream); break;

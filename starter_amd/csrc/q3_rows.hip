@@ -136,18 +136,29 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-// grid (B): reduce argmax partials [nparts, B] -> tokens[b]; block 0 advances *pos.
-__global__ __launch_bounds__(THREADS) void argmax_finish_kernel(const float* pv, const int* pi, int nparts,
-                                                                int B, int64_t* tokens, int64_t* pos) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+// grid (B), 1024 threads: reduce argmax partials [nparts, B] -> tokens[b];
+// block 0 advances *pos.  Each thread reads its partials four at a time with
+// the loads issued together; waves reduce with shuffles, then LDS.
+constexpr int FIN_THREADS = 1024;
+__global__ __launch_bounds__(FIN_THREADS) void argmax_finish_kernel(const float* pv, const int* pi, int nparts,
+                                                                    int B, int64_t* tokens, int64_t* pos) {
+    __shared__ float sv[FIN_THREADS / 64];
+    __shared__ int si[FIN_THREADS / 64];
     const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int p = threadIdx.x; p < nparts; p += THREADS) {
-        const float v = pv[p * B + b];
-        const int i = pi[p * B + b];
-        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    for (int p0 = threadIdx.x; p0 < nparts; p0 += 4 * FIN_THREADS) {
+        float v[4];
+        int ix[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = p0 + j * FIN_THREADS;
+            v[j] = p < nparts ? pv[p * B + b] : -INFINITY;
+            ix[j] = p < nparts ? pi[p * B + b] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (better(v[j], ix[j], bv, bi)) { bv = v[j]; bi = ix[j]; }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -158,7 +169,7 @@ __global__ __launch_bounds__(THREADS) void argmax_finish_kernel(const float* pv,
     if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < FIN_THREADS / 64; ++w)
             if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
         tokens[b] = bi;
         if (pos && b == 0) *pos += 1;
@@ -245,8 +256,8 @@ extern "C" int q3_qk_norm_rope_kv(const bf16_t* qkv, int ld_qkv, const bf16_t* q
 extern "C" int q3_argmax_finish(const float* part_val, const int* part_idx, int nparts, int B, int64_t* tokens,
                                 int64_t* pos, hipStream_t stream) {
     if (nparts < 1 || B < 1 || !part_val || !part_idx || !tokens) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(THREADS), 0, stream, part_val, part_idx, nparts, B,
-                       tokens, pos);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(FIN_THREADS), 0, stream, part_val, part_idx, nparts,
+                       B, tokens, pos);
     Q3_CHECK_LAUNCH();
 }
 

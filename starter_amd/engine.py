@@ -40,7 +40,7 @@ For B > 8 the projections run on the MFMA GEMM with separate norm kernels.
 from __future__ import annotations
 
 import ctypes
-import os
+import sys
 import time
 
 import numpy as np
@@ -67,7 +67,8 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _log(msg: str) -> None:
-    print(f"[engine] {msg}", flush=True)
+    # stderr: stdout belongs to the caller (bench.py prints one JSON line there).
+    print(f"[engine] {msg}", file=sys.stderr, flush=True)
 
 
 def rope_tables(theta: float, head_dim: int, length: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -96,7 +97,10 @@ def _check_ids(input_ids, vocab: int) -> torch.Tensor:
 
 
 def _bf16(arr: np.ndarray, device: str) -> torch.Tensor:
-    host = torch.from_numpy(np.ascontiguousarray(arr).view(np.int16))
+    a = np.ascontiguousarray(arr)
+    if not a.flags.writeable:  # read-only memory map: torch wants a writable buffer
+        a = a.copy()
+    host = torch.from_numpy(a.view(np.int16))
     return host.to(device, non_blocking=False).view(torch.bfloat16)
 
 
@@ -233,7 +237,7 @@ class Engine:
         self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
         self.small = B <= _lib.GEMV_MAX_M
         if self.small:
-            self.lm_parts = call("q3_gemv_partials", B, V, H)
+            self.lm_parts = call("q3_gemv_partials", B, V, _lib.EPI_ARGMAX)
             self.part_val = self._empty(self.lm_parts, B, dtype=torch.float32)
             self.part_idx = self._empty(self.lm_parts, B, dtype=torch.int32)
         self.logits = self._empty(B, V)
@@ -268,11 +272,11 @@ class Engine:
                 if i == 0:
                     call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
                          resid, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
-                         None, None, s)
+                         None, None, None, None, None, s)
                 else:
                     call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["in_ln"]), self.EPS, None,
                          _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
-                         None, None, s)
+                         None, None, None, None, None, s)
             else:
                 if i == 0:
                     call("q3_embed_rmsnorm", tok, _ptr(self.embed), resid, nbuf, _ptr(L["in_ln"]), B, H,
@@ -283,16 +287,16 @@ class Engine:
                      self.qkv_size, s)
             call("q3_attn_decode", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml), B, Hq, Hkv, C,
-                 self.splits, self.EPS, self.SCALE, s)
+                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml), None, None,
+                 B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
             call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
             if self.small:
                 call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
-                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, s)
+                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
                 call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["post_ln"]), self.EPS, None,
-                     _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, s)
+                     _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, None, None, None, s)
                 call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
-                     B, H, I, _lib.EPI_RESID, resid, H, None, None, s)
+                     B, H, I, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
             else:
                 call("q3_gemm", attn, self.q_size, _ptr(L["o"]), B, H, self.q_size, _lib.EPI_RESID,
                      resid, H, s)
@@ -303,9 +307,8 @@ class Engine:
             epi = _lib.EPI_STORE_ARGMAX if self.keep_logits else _lib.EPI_ARGMAX
             call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(self.final_norm), self.EPS, None,
                  _ptr(self.lm_head), B, V, H, epi, _ptr(self.logits), V, _ptr(self.part_val),
-                 _ptr(self.part_idx), s)
-            call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok,
-                 pos, s)
+                 _ptr(self.part_idx), None, None, None, s)
+            call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
         else:
             call("q3_rmsnorm", resid, H, _ptr(self.final_norm), nbuf, H, B, H, self.EPS, s)
             call("q3_gemm", nbuf, H, _ptr(self.lm_head), B, V, H, _lib.EPI_STORE, _ptr(self.logits), V, s)
@@ -419,7 +422,7 @@ class Engine:
             if B <= _lib.GEMV_MAX_M:
                 call("q3_gemv", _lib.X_NORM, _ptr(last), T * H, None, _ptr(self.final_norm), self.EPS, None,
                      _ptr(self.lm_head), B, self.VOCAB, H, _lib.EPI_STORE, _ptr(logits), self.VOCAB,
-                     None, None, s)
+                     None, None, None, None, None, s)
             else:
                 n_last = self._empty(B, H)
                 call("q3_rmsnorm", _ptr(last), T * H, _ptr(self.final_norm), _ptr(n_last), H, B, H,
@@ -512,6 +515,3 @@ class Engine:
         self._release_graph()
         self.batch = self.capacity = 0
 
-
-def _env_flag(name: str) -> bool:
-    return os.environ.get(name, "") not in ("", "0")

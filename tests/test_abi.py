@@ -50,11 +50,12 @@ def test_error_string():
 def test_bad_arguments_raise_without_launching():
     # M = 0 and K not a multiple of 8 are rejected before any device work.
     with pytest.raises(RuntimeError, match="q3_gemv failed"):
-        _lib.call("q3_gemv", 0, None, 0, None, None, 0.0, None, None, 0, 4, 8, 0, None, 0, None, None, None)
+        _lib.call("q3_gemv", 0, None, 0, None, None, 0.0, None, None, 0, 4, 8, 0, None, 0, None, None, None,
+                  None, None, None)
     with pytest.raises(RuntimeError, match="q3_gemm failed"):
         _lib.call("q3_gemm", None, 0, None, 4, 4, 60, 0, None, 0, None)
     with pytest.raises(RuntimeError, match="q3_attn_decode failed"):
-        _lib.call("q3_attn_decode", None, 0, None, None, None, None, None, None, None, None, None,
+        _lib.call("q3_attn_decode", None, 0, None, None, None, None, None, None, None, None, None, None, None,
                   1, 32, 7, 64, 1, 1e-6, 0.1, None)
 
 
@@ -67,5 +68,6 @@ def test_attention_splits_policy():
 
 
 def test_gemv_partials():
-    assert _lib.call("q3_gemv_partials", 1, 151936, 2560) == 151936 // 4 // 4
-    assert _lib.call("q3_gemv_partials", 8, 151936, 2560) == 151936 // 2 // 4
+    assert _lib.call("q3_gemv_partials", 1, 151936, _lib.EPI_ARGMAX) == 151936 // 4 // 4
+    assert _lib.call("q3_gemv_partials", 8, 151936, _lib.EPI_ARGMAX) == 151936 // 2 // 4
+    assert _lib.call("q3_gemv_partials", 1, 2560, _lib.EPI_STORE) == 2560 // 4

@@ -175,14 +175,15 @@ def test_gemv_plain_store(M, N, K):
     x, w = rnd((M, K), 1.0, M), rnd((N, K), 0.02, N + K)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     call("q3_gemv", _lib.X_PLAIN, P(dv(x)), K, None, None, 0.0, None, P(dv(w)), M, N, K,
-         _lib.EPI_STORE, P(y), N, None, None, S())
+         _lib.EPI_STORE, P(y), N, None, None, None, None, None, S())
     torch.cuda.synchronize()
     check_projection(y, x, w)
 
 
-def gemv(x_mode, x, ldx, w, M, N, K, epi, y, ldy, ids=None, norm_w=None, resid_out=None, pv=None, pi=None):
+def gemv(x_mode, x, ldx, w, M, N, K, epi, y, ldy, ids=None, norm_w=None, resid_out=None, pv=None, pi=None,
+         tokens=None, pos=None, counter=None):
     call("q3_gemv", x_mode, P(x), ldx, P(ids), P(norm_w), 1e-6, P(resid_out), P(w), M, N, K, epi, P(y), ldy,
-         P(pv), P(pi), S())
+         P(pv), P(pi), P(tokens), P(pos), P(counter), S())
 
 
 @pytest.mark.parametrize("M", [1, 3, 8])
@@ -235,7 +236,7 @@ def test_gemv_embed_norm_and_argmax(M):
     assert torch.equal(resid.cpu(), table[ids])
     check_projection(y, n.cpu(), table)
     # Fused argmax partials + finish == argmax of the stored logits (first index on ties).
-    nparts = call("q3_gemv_partials", M, V, K)
+    nparts = call("q3_gemv_partials", M, V, _lib.EPI_ARGMAX)
     pv = torch.empty(nparts, M, dtype=torch.float32, device=DEV)
     pi = torch.empty(nparts, M, dtype=torch.int32, device=DEV)
     y2 = torch.empty_like(y)
@@ -246,10 +247,17 @@ def test_gemv_embed_norm_and_argmax(M):
     tok2 = torch.empty_like(tok)
     gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi)
     call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok2), None, S())
+    # Fused finish: the last workgroup reduces the partials, twice in a row
+    # (the counter must come back to zero).
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tok3 = torch.full_like(tok, -1)
+    for _ in range(2):
+        gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi,
+             tokens=tok3, pos=pos, counter=counter)
     torch.cuda.synchronize()
     assert torch.equal(y2.cpu(), y.cpu())
-    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist() == tok2.cpu().tolist()
-    assert pos.item() == 6
+    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist() == tok2.cpu().tolist() == tok3.cpu().tolist()
+    assert pos.item() == 8 and counter.item() == 0
 
 
 def test_argmax_rows_ties():
@@ -311,10 +319,19 @@ def test_attn_decode(B, C, pos, splits):
     pml = torch.empty(B, Hq, splits, 2, dtype=torch.float32, device=DEV)
     out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
     posd = torch.tensor([pos], dtype=torch.int64, device=DEV)
-    call("q3_attn_decode", P(dv(qkv)), width, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)),
-         P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
+    qkvd, qwd, kwd, cosd, sind = dv(qkv), dv(qw), dv(kw), dv(cos), dv(sin)
+    call("q3_attn_decode", P(qkvd), width, P(qwd), P(kwd), P(cosd), P(sind),
+         P(posd), P(ckd), P(cvd), P(pacc), P(pml), None, None, B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
+    # Fused merge (last workgroup per (b, kv head)), run twice: same bits, counters back at zero.
+    fused = torch.empty_like(out)
+    counter = torch.zeros(B * Hkv, dtype=torch.int32, device=DEV)
+    for _ in range(2):
+        call("q3_attn_decode", P(qkvd), width, P(qwd), P(kwd), P(cosd), P(sind),
+             P(posd), P(ckd), P(cvd), P(pacc), P(pml), P(fused), P(counter), B, Hq, Hkv, C, splits, 1e-6,
+             D ** -0.5, S())
     torch.cuda.synchronize()
+    assert torch.equal(fused.cpu(), out.cpu()) and torch.all(counter == 0)
     x = qkv.view(B, 1, Hq + 2 * Hkv, D)
     c, s_ = cos[pos].view(1, 1, 1, D), sin[pos].view(1, 1, 1, D)
     q = oc.apply_rope(oc.rms_norm(x[:, :, :Hq], qw, 1e-6), c, s_)[:, 0]
