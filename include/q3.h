@@ -68,6 +68,27 @@ int q3_gemv_partials(int M, int N, int epi);
 int q3_gemm(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, hipStream_t stream);
 
+/* Decode projection for 1..64 rows on MFMA, weights streamed from HBM into
+ * MFMA operands: y = epi(x . W^T), epi in {STORE, RESID, SWIGLU}.  Replaces
+ * skinny_linear / skinny_linear_split (fused.py:365,525) at batch 9..64.
+ * N % 64 == 0, K % 256 == 0.  Narrow N splits K over q3_skinny_splits(M, N, K)
+ * workgroup columns; then ws must hold q3_skinny_ws_floats(M, N, K) floats and
+ * a fixed-order reduce kernel (same stream) applies the epilogue. */
+int q3_skinny(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
+              int epi, uint16_t *y, int ldy, float *ws, hipStream_t stream);
+/* q3_skinny on weights repacked by q3_tile16: the same result, but every load
+ * instruction reads 1 KB of contiguous weights. */
+int q3_skinny_tiled(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
+                    int epi, uint16_t *y, int ldy, float *ws, hipStream_t stream);
+/* Repack row-major W [N, K] (N % 16 == 0, K % 32 == 0) into 16-row tiles:
+ * element (n, k) goes to ((n/16 * K/32 + k/32) * 64 + (k%32)/8 * 16 + n%16) * 8
+ * + k%8, the MFMA A-operand order of one wave.  Setup-time layout change for
+ * the weights uploaded at engine init (engine/engine.py:152-175 keeps its fused
+ * weights row-major). */
+int q3_tile16(const uint16_t *w, int N, int K, uint16_t *out, hipStream_t stream);
+int q3_skinny_splits(int M, int N, int K);
+int q3_skinny_ws_floats(int M, int N, int K);
+
 /* Row RMSNorm: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).  rms_norm
  * (rmsnorm.py:48, engine.py:75).  cols % 8 == 0. */
 int q3_rmsnorm(const uint16_t *x, int ldx, const uint16_t *w, uint16_t *y, int ldy,

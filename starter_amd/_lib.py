@@ -30,6 +30,11 @@ SIGNATURES = {
     "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
     "q3_gemv_partials": [_I, _I, _I],
     "q3_gemm": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P],
+    "q3_skinny": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "q3_skinny_tiled": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "q3_tile16": [_P, _I, _I, _P, _P],
+    "q3_skinny_splits": [_I, _I, _I],
+    "q3_skinny_ws_floats": [_I, _I, _I],
     "q3_rmsnorm": [_P, _I, _P, _P, _I, _I, _I, _F, _P],
     "q3_add_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "q3_embed_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
@@ -48,7 +53,7 @@ SIGNATURES = {
 _RESTYPES = {"q3_error_string": ctypes.c_char_p}
 
 #: entry points that return a count, not an error code
-_COUNTS = {"q3_gemv_partials", "q3_attn_splits"}
+_COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_skinny_splits", "q3_skinny_ws_floats"}
 
 _LIB: ctypes.CDLL | None = None
 

@@ -1,0 +1,323 @@
+// Decode projection for 1..64 rows on MFMA: y[m, n] = epi(sum_k x[m, k] * W[n, k]).
+//
+// Reference: engine/engine.py:431-450 (_linear: skinny kernels up to 32 rows,
+// cuBLAS above) and engine/kernels/fused.py:462-550 (split-K with a fixed-order
+// reduction, no atomics).  At batch 16-64 a projection still reads each weight
+// byte once, but the arithmetic (2*M flops per weight) is beyond the VALU, so
+// the weights stream straight from HBM into v_mfma_f32_16x16x32_bf16 A
+// operands:
+//   * a workgroup owns 64 weight rows (16 per wave) and one K range; the four
+//     lanes of a row read 64 contiguous bytes per load instruction, and weight
+//     loads run two 256-element chunks ahead of the MFMAs;
+//   * the batch rows x[0..M) for the chunk are staged once per workgroup in LDS
+//     (16-byte chunks XOR-swizzled by row) and feed all four waves as B operands;
+//   * narrow matrices split K over workgroups; FP32 partials are summed in a
+//     fixed order by q3_skinny_reduce, which applies the epilogue.  With one
+//     split the epilogue runs here.
+// MFMA layout (lane l, g = l/16, n = l%16): A[m=n][k=8g+t] is W row n, B[k][n]
+// is x row n, C[4g+i][n] = (weight row 4g+i, batch row n).  The k slot (g, t)
+// of MFMA step j (0..7) maps to chunk element 32j + 8g + t; A and B use the
+// same map.
+#include "q3_common.hpp"
+#include "q3.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int ROWS = 64;  // weight rows per workgroup (16 per wave)
+constexpr int KC = 256;   // K elements per chunk (two 128-element sub-chunks)
+
+// x tile [16*MT rows][KC] BF16: 32 chunks of 16 bytes per row, swizzled so the
+// 16 rows an operand read touches spread over the banks.
+__device__ __forceinline__ int xsw(int r, int c) { return c ^ (r & 15); }
+
+struct SkinnyArgs {
+    const bf16_t* x;
+    int ldx;
+    const bf16_t* w;
+    int M, N, K, splits, kper;  // kper: K elements per split (multiple of KC)
+    int epi;
+    bf16_t* y;
+    int ldy;
+    float* ws;                  // [splits, M, N] FP32 partials when splits > 1
+};
+
+template <int MT>
+__device__ __forceinline__ void load_x(const SkinnyArgs& a, int k0, uint4 (&xr)[MT * 2]) {
+    // 16*MT rows x 32 chunks = 512*MT chunks over 256 threads.
+#pragma unroll
+    for (int j = 0; j < MT * 2; ++j) {
+        const int e = threadIdx.x + j * THREADS;
+        const int r = e >> 5, c = e & 31;
+        xr[j] = make_uint4(0, 0, 0, 0);
+        if (r < a.M) xr[j] = *reinterpret_cast<const uint4*>(a.x + (int64_t)r * a.ldx + k0 + 8 * c);
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void store_x(bf16_t* xs, const uint4 (&xr)[MT * 2]) {
+#pragma unroll
+    for (int j = 0; j < MT * 2; ++j) {
+        const int e = threadIdx.x + j * THREADS;
+        const int r = e >> 5, c = e & 31;
+        *reinterpret_cast<uint4*>(xs + r * KC + xsw(r, c) * 8) = xr[j];
+    }
+}
+
+// Weight chunk of this lane: row (row0 + n), 16-byte pieces at elements
+// k0 + 32j + 8g (j = 0..7), so each load instruction covers 64 contiguous
+// bytes of each of the wave's 16 rows.
+__device__ __forceinline__ void load_w(const bf16_t* wrow, int k0, int g, uint4 (&wr)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wr[j] = load_nt(wrow + k0 + 32 * j + 8 * g);
+}
+
+// Same chunk from the 16-row tiled layout: the 16x32 block b of tile t is 1 KB
+// at ((t * K/32) + b) * 512 elements, lane l = 16g + n at 8l, so each load
+// instruction reads 1 KB contiguous.
+__device__ __forceinline__ void load_w_tiled(const bf16_t* wtile, int k0, int lane, uint4 (&wr)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wr[j] = load_nt(wtile + (int64_t)(k0 / 32 + j) * 512 + lane * 8);
+}
+
+// NCH chunks per split, fully unrolled: weight loads run two chunks ahead in a
+// three-slot register ring, x one chunk ahead through a double-buffered LDS
+// tile.  Loads are issued x(c+1) then W(c+2), so storing x(c+1) waits only for
+// loads issued before it and W(c+2) stays in flight (vector memory counters
+// retire in order).
+template <int MT, int NCH, bool TILED>
+__global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
+    __shared__ __align__(16) bf16_t xs[2][16 * MT * KC];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const int row0 = blockIdx.x * ROWS + wave * 16;
+    const int split = blockIdx.y;
+    const int kbeg = split * a.kper;
+    const int kend = min(kbeg + a.kper, a.K);
+    const bool active = row0 < a.N;
+    const bf16_t* wrow = TILED ? a.w + (int64_t)min(row0, a.N - 16) / 16 * (a.K / 32) * 512
+                               : a.w + (int64_t)min(row0 + n, a.N - 1) * a.K;
+    auto load = [&](int k, uint4(&wr)[8]) {
+        if (TILED) load_w_tiled(wrow, k, lane, wr);
+        else load_w(wrow, k, g, wr);
+    };
+    if (kbeg >= a.K) {
+        // A split past the end of K contributes zeros (uniform exit: no barrier pending).
+        if (a.splits > 1 && active)
+            for (int m = n; m < a.M; m += 16)
+                *reinterpret_cast<float4*>(a.ws + ((int64_t)split * a.M + m) * a.N + row0 + 4 * g) =
+                    make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    uint4 w[3][8], xr[MT * 2];
+    load_x<MT>(a, kbeg, xr);
+    if (active) load(kbeg, w[0]);
+    if (active && kbeg + KC < kend) load(kbeg + KC, w[1]);
+    store_x<MT>(xs[0], xr);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int k0 = kbeg + c * KC;
+        if (k0 < kend) {
+            const bool nx = k0 + KC < kend;
+            if (nx) load_x<MT>(a, k0 + KC, xr);
+            if (active && k0 + 2 * KC < kend) load(k0 + 2 * KC, w[(c + 2) % 3]);
+            if (active) {
+                const bf16_t* xb = xs[c & 1];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bf16x8_t av = as_bf16x8(w[c % 3][j]);
+                    const int ch = 4 * j + g;  // 16-byte chunk of the x row
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const int r = 16 * t + n;
+                        const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const uint4*>(xb + r * KC + xsw(r, ch) * 8));
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
+                    }
+                }
+            }
+            if (nx) store_x<MT>(xs[(c + 1) & 1], xr);
+            __syncthreads();
+        }
+    }
+    if (!active) return;
+
+    // acc[t][i] = partial (weight row row0 + 4g + i, batch row 16t + n).
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + n;
+        if (m >= a.M) continue;
+        const int r = row0 + 4 * g;
+        if (a.splits > 1) {
+            float* dst = a.ws + ((int64_t)split * a.M + m) * a.N + r;
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        } else if (a.epi == Q3_EPI_SWIGLU) {
+            bf16_t* dst = a.y + (int64_t)m * a.ldy + (r >> 1);
+            dst[0] = (bf16_t)f2bf(silu_bf16(rbf(acc[t][0])) * rbf(acc[t][1]));
+            dst[1] = (bf16_t)f2bf(silu_bf16(rbf(acc[t][2])) * rbf(acc[t][3]));
+        } else if (a.epi == Q3_EPI_RESID) {
+            bf16_t* dst = a.y + (int64_t)m * a.ldy + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = (bf16_t)f2bf(bf2f(dst[i]) + rbf(acc[t][i]));
+        } else {
+            bf16_t* dst = a.y + (int64_t)m * a.ldy + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = (bf16_t)f2bf(acc[t][i]);
+        }
+    }
+}
+
+// Fixed-order sum of the split partials, then the epilogue.  One thread per
+// (batch row, output pair).
+__global__ __launch_bounds__(THREADS) void skinny_reduce_kernel(const float* ws, int splits, int M, int N, int epi,
+                                                                bf16_t* y, int ldy) {
+    const int64_t e = (int64_t)blockIdx.x * THREADS + threadIdx.x;  // pair index
+    const int pairs = N / 2;
+    if (e >= (int64_t)M * pairs) return;
+    const int m = (int)(e / pairs), c = 2 * (int)(e % pairs);
+    float v0 = 0.f, v1 = 0.f;
+    for (int s = 0; s < splits; ++s) {
+        const float2 p = *reinterpret_cast<const float2*>(ws + ((int64_t)s * M + m) * N + c);
+        v0 += p.x;
+        v1 += p.y;
+    }
+    if (epi == Q3_EPI_SWIGLU) {
+        y[(int64_t)m * ldy + (c >> 1)] = (bf16_t)f2bf(silu_bf16(rbf(v0)) * rbf(v1));
+    } else if (epi == Q3_EPI_RESID) {
+        bf16_t* dst = y + (int64_t)m * ldy + c;
+        dst[0] = (bf16_t)f2bf(bf2f(dst[0]) + rbf(v0));
+        dst[1] = (bf16_t)f2bf(bf2f(dst[1]) + rbf(v1));
+    } else {
+        y[(int64_t)m * ldy + c] = (bf16_t)f2bf(v0);
+        y[(int64_t)m * ldy + c + 1] = (bf16_t)f2bf(v1);
+    }
+}
+
+template <int MT, bool TILED>
+int launch_nch(int nch, dim3 grid, const SkinnyArgs& a, hipStream_t stream) {
+    switch (nch) {
+#define Q3_SK(n) \
+    case n: hipLaunchKernelGGL((skinny_kernel<MT, n, TILED>), grid, dim3(THREADS), 0, stream, a); return 0;
+        Q3_SK(1) Q3_SK(2) Q3_SK(3) Q3_SK(4) Q3_SK(5) Q3_SK(6) Q3_SK(8) Q3_SK(10)
+#undef Q3_SK
+    }
+    return -1;
+}
+
+template <bool TILED>
+int launch_mt(int mt, int nch, dim3 grid, const SkinnyArgs& a, hipStream_t stream) {
+    switch (mt) {
+        case 1: return launch_nch<1, TILED>(nch, grid, a, stream);
+        case 2: return launch_nch<2, TILED>(nch, grid, a, stream);
+        case 3: return launch_nch<3, TILED>(nch, grid, a, stream);
+        case 4: return launch_nch<4, TILED>(nch, grid, a, stream);
+    }
+    return -1;
+}
+
+// Row-major [N, K] -> 16-row tiled: one thread per 16-byte piece of the output.
+__global__ __launch_bounds__(THREADS) void tile16_kernel(const bf16_t* w, int N, int K, bf16_t* out) {
+    const int64_t p = (int64_t)blockIdx.x * THREADS + threadIdx.x;
+    const int kb = K / 32;
+    if (p >= (int64_t)N / 16 * kb * 64) return;
+    const int l = (int)(p & 63);
+    const int64_t blk = p >> 6;
+    const int t = (int)(blk / kb), b = (int)(blk % kb);
+    const int n = 16 * t + (l & 15), k = 32 * b + 8 * (l >> 4);
+    *reinterpret_cast<uint4*>(out + p * 8) = *reinterpret_cast<const uint4*>(w + (int64_t)n * K + k);
+}
+
+}  // namespace
+
+// Chunks per split (compile-time in the kernel).
+constexpr int NCH_OPTIONS[] = {1, 2, 3, 4, 5, 6, 8, 10};
+
+extern "C" int q3_skinny_splits(int M, int N, int K) {
+    // More splits give more workgroups (target >= 512, two per CU) but cost
+    // FP32 partial traffic of 8*splits*M*N bytes (write + read) against the
+    // weights' 2*N*K; keep that under ~20%.  Each split keeps >= 2 chunks.
+    const int tiles = (N + ROWS - 1) / ROWS;
+    const int chunks = K / KC;
+    int best = 1;
+    for (int s = 2; s <= 16 && tiles * best < 512; ++s) {
+        if (chunks / s < 2) break;
+        const int nch = (chunks + s - 1) / s;
+        bool ok = false;
+        for (int o : NCH_OPTIONS) ok |= (o == nch);
+        if (!ok) continue;
+        if (4.0 * s * M > 0.2 * K) break;
+        best = s;
+    }
+    // The unsplit kernel must also fit a compile-time chunk count.
+    if (best == 1) {
+        bool ok = false;
+        for (int o : NCH_OPTIONS) ok |= (o == chunks);
+        if (!ok) {
+            for (int s = 2; s <= chunks; ++s) {
+                const int nch = (chunks + s - 1) / s;
+                bool fit = false;
+                for (int o : NCH_OPTIONS) fit |= (o == nch);
+                if (fit) return s;
+            }
+        }
+    }
+    return best;
+}
+
+extern "C" int q3_skinny_ws_floats(int M, int N, int K) {
+    const int s = q3_skinny_splits(M, N, K);
+    return s > 1 ? s * M * N : 0;
+}
+
+namespace {
+
+int skinny_launch(bool tiled, const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
+                  int ldy, float* ws, hipStream_t stream) {
+    if (M < 1 || M > 64 || N < 1 || N % 64 || K < KC || K % KC || ldx % 8 || !x || !w || !y ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15))
+        return (int)hipErrorInvalidValue;
+    if (epi != Q3_EPI_STORE && epi != Q3_EPI_RESID && epi != Q3_EPI_SWIGLU) return (int)hipErrorInvalidValue;
+    const int splits = q3_skinny_splits(M, N, K);
+    if (splits > 1 && !ws) return (int)hipErrorInvalidValue;
+    const int chunks = K / KC;
+    const int kper = (chunks + splits - 1) / splits * KC;
+    SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws};
+    const dim3 grid(N / ROWS, splits);
+    const int mt = (M + 15) / 16;
+    const int nch = kper / KC;
+    const int bad = tiled ? launch_mt<true>(mt, nch, grid, a, stream) : launch_mt<false>(mt, nch, grid, a, stream);
+    if (bad) return (int)hipErrorInvalidValue;
+    hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess || splits == 1) return (int)rc;
+    const int64_t pairs = (int64_t)M * (N / 2);
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((pairs + THREADS - 1) / THREADS)), dim3(THREADS), 0,
+                       stream, ws, splits, M, N, epi, y, ldy);
+    Q3_CHECK_LAUNCH();
+}
+
+}  // namespace
+
+extern "C" int q3_skinny(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
+                         int ldy, float* ws, hipStream_t stream) {
+    return skinny_launch(false, x, ldx, w, M, N, K, epi, y, ldy, ws, stream);
+}
+
+extern "C" int q3_skinny_tiled(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, int epi, bf16_t* y,
+                               int ldy, float* ws, hipStream_t stream) {
+    return skinny_launch(true, x, ldx, wt, M, N, K, epi, y, ldy, ws, stream);
+}
+
+extern "C" int q3_tile16(const bf16_t* w, int N, int K, bf16_t* out, hipStream_t stream) {
+    if (N < 16 || N % 16 || K < 32 || K % 32 || !w || !out ||
+        ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15))
+        return (int)hipErrorInvalidValue;
+    const int64_t pieces = (int64_t)N / 16 * (K / 32) * 64;
+    hipLaunchKernelGGL(tile16_kernel, dim3((unsigned)((pieces + THREADS - 1) / THREADS)), dim3(THREADS), 0, stream, w,
+                       N, K, out);
+    Q3_CHECK_LAUNCH();
+}

@@ -34,7 +34,8 @@ Decode step (one hipGraph, self-feeding like reference ``:805-839``), B <= 8:
   gemv(o, +residual) | gemv(norm -> gate_up -> SwiGLU) | gemv(down, +residual) |
   gemv(norm -> qkv of the next layer) ... | gemv(norm -> lm_head -> argmax
   partials) | argmax finish (token -> input buffer, pos += 1).
-For B > 8 the projections run on the MFMA GEMM with separate norm kernels.
+For B > GEMV_BATCH_MAX the projections stream 16-row tiled weight copies into
+MFMA (B <= 64) or run on the LDS-tiled MFMA GEMM, with separate norm kernels.
 """
 
 from __future__ import annotations
@@ -60,6 +61,13 @@ PREFILL_CHUNK_TOKENS = 131072
 
 #: Headroom kept free when sizing the KV cache.
 MEMORY_MARGIN_BYTES = 2 << 30
+
+#: Largest decode batch on the dot2 GEMVs (fused norm prologue and argmax
+#: epilogue).  Above it, up to SKINNY_BATCH_MAX, projections stream 16-row
+#: tiled weight copies into MFMA (``q3_skinny_tiled``), which at 5+ rows beats
+#: the GEMV's VALU-bound dot products; above that the LDS-tiled GEMM.
+GEMV_BATCH_MAX = 4
+SKINNY_BATCH_MAX = 64
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -165,6 +173,7 @@ class Engine:
         self.cos_table = self.sin_table = None
         self._grow_rope(4096)
 
+        self.tiled = None  # 16-row tiled weight copies, made on first use
         self.batch = 0
         self.capacity = 0
         self.cache_k = self.cache_v = None
@@ -235,13 +244,40 @@ class Engine:
         self.act = self._empty(B, self.INTER)
         self.part_acc = self._empty(B, self.HEADS, self.splits, D, dtype=torch.float32)
         self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
-        self.small = B <= _lib.GEMV_MAX_M
+        self.small = B <= GEMV_BATCH_MAX
+        self.skinny = not self.small and B <= SKINNY_BATCH_MAX
+        # Split-K workspace of the MFMA decode projections.
+        ws = 0
+        if self.skinny:
+            self._make_tiled()
+            for N, K in ((self.qkv_size, H), (H, self.q_size), (2 * self.INTER, H), (H, self.INTER), (V, H)):
+                ws = max(ws, call("q3_skinny_ws_floats", B, N, K))
+        self.skinny_ws = self._empty(max(ws, 1), dtype=torch.float32)
         if self.small:
             self.lm_parts = call("q3_gemv_partials", B, V, _lib.EPI_ARGMAX)
             self.part_val = self._empty(self.lm_parts, B, dtype=torch.float32)
             self.part_idx = self._empty(self.lm_parts, B, dtype=torch.int32)
         self.logits = self._empty(B, V)
         self._capture()
+
+    def _make_tiled(self) -> None:
+        """16-row tiled copies of every decode weight (``q3_tile16``), kept for the
+        engine's lifetime: 8 GB next to the row-major set, which the GEMVs and the
+        prefill GEMM read."""
+        if self.tiled is not None:
+            return
+        t0 = time.monotonic()
+        tiled = {}
+        with torch.cuda.stream(self.stream):
+            for w in [self.lm_head] + [L[k] for L in self.layers for k in ("qkv", "o", "gate_up", "down")]:
+                if id(w) in tiled or w.shape[0] % 16 or w.shape[1] % 32:
+                    continue
+                t = torch.empty_like(w)
+                call("q3_tile16", _ptr(w), w.shape[0], w.shape[1], _ptr(t), self._s)
+                tiled[id(w)] = t
+        self.stream.synchronize()
+        self.tiled = tiled
+        _log(f"tiled weight copies made in {time.monotonic() - t0:.2f}s")
 
     def _release_graph(self) -> None:
         if self.graph is not None:
@@ -283,8 +319,7 @@ class Engine:
                          self.EPS, s)
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
-                call("q3_gemm", nbuf, H, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv,
-                     self.qkv_size, s)
+                self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
             call("q3_attn_decode", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
                  vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml), None, None,
@@ -298,11 +333,10 @@ class Engine:
                 call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
                      B, H, I, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
             else:
-                call("q3_gemm", attn, self.q_size, _ptr(L["o"]), B, H, self.q_size, _lib.EPI_RESID,
-                     resid, H, s)
+                self._proj(attn, self.q_size, L["o"], H, self.q_size, _lib.EPI_RESID, resid, H)
                 call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), nbuf, H, B, H, self.EPS, s)
-                call("q3_gemm", nbuf, H, _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, s)
-                call("q3_gemm", act, I, _ptr(L["down"]), B, H, I, _lib.EPI_RESID, resid, H, s)
+                self._proj(nbuf, H, L["gate_up"], 2 * I, H, _lib.EPI_SWIGLU, act, I)
+                self._proj(act, I, L["down"], H, I, _lib.EPI_RESID, resid, H)
         if self.small:
             epi = _lib.EPI_STORE_ARGMAX if self.keep_logits else _lib.EPI_ARGMAX
             call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(self.final_norm), self.EPS, None,
@@ -311,8 +345,18 @@ class Engine:
             call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
         else:
             call("q3_rmsnorm", resid, H, _ptr(self.final_norm), nbuf, H, B, H, self.EPS, s)
-            call("q3_gemm", nbuf, H, _ptr(self.lm_head), B, V, H, _lib.EPI_STORE, _ptr(self.logits), V, s)
+            self._proj(nbuf, H, self.lm_head, V, H, _lib.EPI_STORE, _ptr(self.logits), V)
             call("q3_argmax_rows", _ptr(self.logits), V, B, V, tok, pos, s)
+
+    def _proj(self, x: int, ldx: int, w: torch.Tensor, N: int, K: int, epi: int, y: int, ldy: int) -> None:
+        """Decode projection above GEMV_BATCH_MAX: the weight-streaming MFMA kernel on
+        the tiled copy where the shape tiles (N % 64, K % 256) and B <= 64, the
+        LDS-tiled MFMA GEMM otherwise."""
+        if self.skinny and N % 64 == 0 and K % 256 == 0:
+            call("q3_skinny_tiled", x, ldx, _ptr(self.tiled[id(w)]), self.batch, N, K, epi, y, ldy,
+                 _ptr(self.skinny_ws), self._s)
+        else:
+            call("q3_gemm", x, ldx, _ptr(w), self.batch, N, K, epi, y, ldy, self._s)
 
     def _capture(self) -> None:
         """Warm every kernel eagerly, then record one decode step as a hipGraph.

@@ -389,3 +389,46 @@ def test_graph_capture_replays_self_feeding_step():
     stream.synchronize()
     call("q3_graph_destroy", ex.value)
     assert tok.item() == 2 and pos.item() == 3
+
+
+@pytest.mark.parametrize("N,K", [(16, 32), (48, 96), (2560, 9728)])
+def test_tile16_layout(N, K):
+    """(n, k) -> ((n/16 * K/32 + k/32) * 64 + (k%32)/8 * 16 + n%16) * 8 + k%8."""
+    w = torch.arange(N * K, dtype=torch.int32).remainder(65521).to(torch.int16).view(torch.bfloat16).reshape(N, K)
+    out = torch.empty_like(dv(w))
+    call("q3_tile16", P(dv(w)), N, K, P(out), S())
+    torch.cuda.synchronize()
+    want = w.view(torch.int16).reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(N, K)
+    assert torch.equal(out.cpu().view(torch.int16), want)
+    n, k = N - 3, K - 7  # one element by the closed form
+    flat = out.cpu().view(torch.int16).reshape(-1)
+    assert flat[((n // 16 * (K // 32) + k // 32) * 64 + (k % 32) // 8 * 16 + n % 16) * 8 + k % 8] == w.view(torch.int16)[n, k]
+
+
+@pytest.mark.parametrize("M", [1, 5, 9, 16, 17, 33, 64])
+@pytest.mark.parametrize("N,K", [(128, 256), (192, 768), (512, 1024), (2560, 4096), (6144, 2560), (2560, 9728)])
+def test_skinny(M, N, K):
+    """Weight-streaming MFMA projection (split-K + fixed-order reduce on narrow N)."""
+    x, w = rnd((M, K), 1.0, M + 7), rnd((N, K), 0.02, N + K + 7)
+    xd, wd = dv(x), dv(w)
+    ws = torch.empty(max(1, call("q3_skinny_ws_floats", M, N, K)), dtype=torch.float32, device=DEV)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    call("q3_skinny", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(y), N, P(ws), S())
+    torch.cuda.synchronize()
+    check_projection(y, x, w)
+    # The tiled layout feeds the same operands in the same order: identical bits.
+    wt = torch.empty_like(wd)
+    call("q3_tile16", P(wd), N, K, P(wt), S())
+    yt = torch.empty_like(y)
+    call("q3_skinny_tiled", P(xd), K, P(wt), M, N, K, _lib.EPI_STORE, P(yt), N, P(ws), S())
+    torch.cuda.synchronize()
+    assert torch.equal(yt, y)
+    res = rnd((M, N), 1.0, 9)
+    resd = dv(res)
+    call("q3_skinny", P(xd), K, P(wd), M, N, K, _lib.EPI_RESID, P(resd), N, P(ws), S())
+    act = torch.empty(M, N // 2, dtype=torch.bfloat16, device=DEV)
+    call("q3_skinny", P(xd), K, P(wd), M, N, K, _lib.EPI_SWIGLU, P(act), N // 2, P(ws), S())
+    torch.cuda.synchronize()
+    yc = y.cpu()
+    assert torch.equal(resd.cpu(), res + yc)
+    assert_nearly_exact(act, oc.swiglu(yc[:, 0::2], yc[:, 1::2]), frac=5e-3)
