@@ -122,16 +122,13 @@ int q3_qk_norm_rope_kv(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w
  * sequence), with the q/k RMSNorm + RoPE and the KV append of that token fused
  * in.  qkv [B, ld_qkv] (q | k | v); cache_k/v [B, Hkv, capacity, 128].
  * Writes per-split partials part_acc [B, Hq, splits, 128] (FP32, unnormalised)
- * and part_ml [B, Hq, splits, 2] (running max, sum).  With out != NULL the
- * last workgroup of each (sequence, KV head) merges the splits into
- * out [B, Hq*128] (BF16), using counter [B*Hkv] (device ints, zero before the
- * first call, left zero); otherwise finish with q3_attn_merge.
+ * and part_ml [B, Hq, splits, 2] (running max, sum); q3_attn_merge finishes.
+ * Any splits >= 1 is valid; q3_attn_splits gives the tuned count.
  * decode_attention_gqa / _split (fused.py:641-846). */
 int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w,
                    const uint16_t *k_norm_w, const uint16_t *cos_table,
                    const uint16_t *sin_table, const int64_t *pos,
                    uint16_t *cache_k, uint16_t *cache_v, float *part_acc, float *part_ml,
-                   uint16_t *out, int *counter,
                    int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                    hipStream_t stream);
 /* Log-sum-exp merge of the splits: out [B, Hq*128] BF16 (fused.py:793-823). */

@@ -27,10 +27,16 @@ constexpr int GROUP = 4;     // query heads per KV head
 constexpr int BLK = 32;      // keys per block
 constexpr int THREADS = 256; // 4 waves
 
-// LDS V tile [32 keys][128 d] BF16, 16-byte chunks swizzled so the column
-// reads for keys kappa(g, t) hit four distinct bank groups.
+// Decode K/V tiles in LDS: [32 keys][16 chunks of 16 bytes], chunk c of key r
+// stored at slot c ^ (r & 15).  Rows arrive whole (1 KB = four keys per load
+// instruction); K operand reads (16 keys at one chunk) and the transposed V
+// reads then spread over all banks.
+__device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
+
+// LDS V tile of the prefill kernel [32 keys][128 d] BF16, 16-byte chunks
+// swizzled so the column reads for keys kappa(g, t) hit four distinct bank groups.
 __device__ __forceinline__ int v_chunk(int key, int c) { return c ^ (((key >> 2) & 3) << 2); }
-// LDS K tile [32 keys][128 d]: rows read 16 at a time at one chunk.
+// LDS K tile of the prefill kernel [32 keys][128 d]: rows read 16 at a time at one chunk.
 __device__ __forceinline__ int k_chunk(int key, int c) { return c ^ (key & 15); }
 
 __device__ __forceinline__ int kappa(int g, int t) { return t < 4 ? 4 * g + t : 16 + 4 * g + (t - 4); }
@@ -47,6 +53,24 @@ __device__ __forceinline__ bf16x8_t vt_operand(const bf16_t* vs, int dm, int n, 
     }
     uint4 v = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
     return as_bf16x8(v);
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+#define Q3_LDS(p) ((__attribute__((address_space(3))) i16x4_t*)(p))
+
+// The same operand from a decode V tile with two ds_read_b64_tr_b16: within
+// each 16-lane group, lane i names 4 consecutive d of one key (key 4*(i/4) +
+// base, d = 16dm + 4*(i%4)); the transpose hands lane n the element d = 16dm + n
+// of the four keys.  Keys 4g..4g+3 fill k slots 0-3, keys 16+4g.. slots 4-7.
+__device__ __forceinline__ bf16x8_t vt_operand_tr(const bf16_t* vt, int dm, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int c = 2 * dm + ((i & 3) >> 1), half = (i & 1) * 4;
+    const int r0 = 4 * g + (i >> 2), r1 = r0 + 16;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r0, c) * 8 + half));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r1, c) * 8 + half));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8_t, v);
 }
 
 // B operand (P^T) from the two score blocks held by this lane.
@@ -115,34 +139,29 @@ struct DecodeArgs {
     bf16_t* cache_v;
     float* part_acc;
     float* part_ml;
-    bf16_t* out;   // fused merge target [B, Hq*D] (optional)
-    int* counter;  // [B*Hkv] arrival counters for the fused merge
     int Hq, Hkv, capacity, splits;
     float eps, scale;
 };
 
-// One 32-key block of K (as MFMA A operands) and V (raw rows) for a wave.
-struct KVBlock {
-    uint4 k[2][4];
-    uint4 v[8];
+// One 32-key block of K and V rows in registers: load j covers keys 4j..4j+3
+// whole, lane l holding chunk (l % 16) ^ (key & 15) of key 4j + l / 16, which is
+// exactly its slot in the LDS tile.
+struct KVRegs {
+    u32x4_t k[8];  // native vectors: HIP's uint4 struct copies as a memcpy and
+    u32x4_t v[8];  // would keep the sets in scratch memory
 };
 
-// Loads keys blk..blk+31 that lie below `limit` (rows past it read as zero).
-__device__ __forceinline__ void load_block(KVBlock& kb, const bf16_t* kbase, const bf16_t* vbase, int blk,
-                                           int limit, int g, int n) {
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-        const int key = blk + 16 * hb + n;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-            kb.k[hb][kk] = key < limit ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + 32 * g + 8 * kk)
-                                       : make_uint4(0, 0, 0, 0);
-    }
+// Rows at or past `last` read row `last` instead (always inside the cache);
+// their scores are masked, so what they hold never reaches the output.
+__device__ __forceinline__ void load_kv(KVRegs& r, const bf16_t* kbase, const bf16_t* vbase, int blk, int last,
+                                        int lane) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int key = blk + 4 * j + g;
-        kb.v[j] = key < limit ? *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + 8 * n)
-                              : make_uint4(0, 0, 0, 0);
+        const int key = 4 * j + (lane >> 4);
+        const int c = (lane & 15) ^ (key & 15);
+        const int64_t off = (int64_t)min(blk + key, last) * D + 8 * c;
+        r.k[j] = *reinterpret_cast<const u32x4_t*>(kbase + off);
+        r.v[j] = *reinterpret_cast<const u32x4_t*>(vbase + off);
     }
 }
 
@@ -154,21 +173,71 @@ __device__ __forceinline__ int split_len(int capacity, int splits) {
     return (per + BLK - 1) / BLK * BLK;
 }
 
+struct WaveState {
+    bf16x8_t qb[4];
+    f32x4_t acc[8];
+    float m, l;
+};
+
+// One 32-key block: registers -> this wave's LDS tiles (the new token's row
+// substituted), S^T = K.Q^T, online softmax, O^T += V^T.P^T.
+__device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf16_t* kt, bf16_t* vt, int blk,
+                                             int end, int sub_row, const bf16_t* knew, const bf16_t* vnew,
+                                             float scale, int lane) {
+    const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        reinterpret_cast<u32x4_t*>(kt)[64 * j + lane] = r.k[j];
+        reinterpret_cast<u32x4_t*>(vt)[64 * j + lane] = r.v[j];
+    }
+    if (sub_row >= 0) {  // the appended token replaces whatever the cache held at pos
+        if (lane < 16) {
+            reinterpret_cast<u32x4_t*>(kt)[kv_slot(sub_row, lane)] = reinterpret_cast<const u32x4_t*>(knew)[lane];
+            reinterpret_cast<u32x4_t*>(vt)[kv_slot(sub_row, lane)] = reinterpret_cast<const u32x4_t*>(vnew)[lane];
+        }
+    }
+    f32x4_t s[2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+        s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const int key = 16 * hb + n;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const u32x4_t kv = reinterpret_cast<const u32x4_t*>(kt)[kv_slot(key, 4 * kk + g)];
+            s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), st.qb[kk], s[hb], 0,
+                                                            0, 0);
+        }
+    }
+    float s0[4], s1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s0[i] = (blk + 4 * g + i < end) ? s[0][i] * scale : -INFINITY;
+        s1[i] = (blk + 16 + 4 * g + i < end) ? s[1][i] * scale : -INFINITY;
+    }
+    const float alpha = softmax_block(s0, s1, st.m, st.l);
+    const bf16x8_t pb = p_operand(s0, s1);
+#pragma unroll
+    for (int dm = 0; dm < 8; ++dm) {
+        st.acc[dm] *= alpha;
+        st.acc[dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand_tr(vt, dm, lane), pb, st.acc[dm], 0, 0, 0);
+    }
+}
+
 // grid (splits, Hkv, B); wave w of a workgroup takes blocks w, w+4, ... of the
-// split's key range; the four waves merge through LDS, then the splits merge
-// in the last-arriving workgroup (or in attn_merge_kernel when out == NULL).
-__global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
+// split's key range with two register sets in flight (the loop is unrolled by
+// two so neither set is ever copied: a copy would wait for the newest loads,
+// as vector memory counters retire in order); the four waves merge through
+// LDS; attn_merge_kernel merges the splits.
+__global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
 
+    __shared__ __align__(16) bf16_t tiles[4][2][BLK * D];  // per wave: K tile, V tile
     __shared__ __align__(16) bf16_t qs[GROUP][D];
     __shared__ __align__(16) bf16_t knew[D];
     __shared__ __align__(16) bf16_t vnew[D];
-    __shared__ __align__(16) bf16_t vs_all[4][BLK * D];
     __shared__ float mm[4][GROUP], ll[4][GROUP];
-    __shared__ float macc[4][GROUP][D];
-    __shared__ int s_last;
 
     const int per = split_len(a.capacity, a.splits);
     const int begin = split * per;
@@ -183,9 +252,9 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
     const float q_lo = bf2f(qrow[lane]), q_hi = bf2f(qrow[lane + 64]);
     const bf16_t* krow = row + a.Hq * D + kvh * D;
     const bf16_t* vrow = row + (a.Hq + a.Hkv) * D + kvh * D;
-    KVBlock cur;
+    KVRegs ra, rb;
     const int first = begin + w * BLK;
-    if (first < range_end) load_block(cur, kbase, vbase, first, range_end, g, n);
+    if (first < range_end) load_kv(ra, kbase, vbase, first, range_end - 1, lane);
 
     const bool bad_pos = pos_raw < 0 || pos_raw >= a.capacity;
     const int pos = bad_pos ? 0 : pos_raw;
@@ -221,78 +290,57 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
 
-    float m = -INFINITY, l = 0.f;
-    f32x4_t acc[8];
+    WaveState st;
+    st.m = -INFINITY;
+    st.l = 0.f;
 #pragma unroll
-    for (int dm = 0; dm < 8; ++dm) acc[dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dm = 0; dm < 8; ++dm) st.acc[dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bf16_t* kt = tiles[w][0];
+    bf16_t* vt = tiles[w][1];
 
     if (first < end) {
-        // Q^T operands, one per 32-wide slice of d: Q[n][32g + 8kk + t].
-        bf16x8_t qb[4];
+        // Q^T operands, one per 32-wide slice of d: Q[n][32kk + 8g + t].
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             uint4 v = make_uint4(0, 0, 0, 0);
-            if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * g + 8 * kk]);
-            qb[kk] = as_bf16x8(v);
+            if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * kk + 8 * g]);
+            st.qb[kk] = as_bf16x8(v);
         }
-        bf16_t* vs = vs_all[w];
-        for (int blk = first; blk < end; blk += 4 * BLK) {
-            KVBlock nxt;
-            const int nb = blk + 4 * BLK;
-            if (nb < end) load_block(nxt, kbase, vbase, nb, end, g, n);
-            // The appended token replaces whatever the cache held at pos.
-            if (owner && blk <= pos && pos < blk + BLK) {
-#pragma unroll
-                for (int hb = 0; hb < 2; ++hb)
-                    if (blk + 16 * hb + n == pos)
-#pragma unroll
-                        for (int kk = 0; kk < 4; ++kk)
-                            cur.k[hb][kk] = *reinterpret_cast<const uint4*>(&knew[32 * g + 8 * kk]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (blk + 4 * j + g == pos) cur.v[j] = reinterpret_cast<const uint4*>(vnew)[n];
-            }
-            // V rows into this wave's LDS tile; rows at or past `end` are zero.
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int r = 4 * j + g;
-                const uint4 v = (blk + r < end) ? cur.v[j] : make_uint4(0, 0, 0, 0);
-                *reinterpret_cast<uint4*>(vs + r * D + v_chunk(r, n) * 8) = v;
-            }
-            f32x4_t s[2];
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
-                    s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.k[hb][kk]), qb[kk], s[hb], 0, 0, 0);
-            }
-            float s0[4], s1[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s0[i] = (blk + 4 * g + i < end) ? s[0][i] * a.scale : -INFINITY;
-                s1[i] = (blk + 16 + 4 * g + i < end) ? s[1][i] * a.scale : -INFINITY;
-            }
-            const float alpha = softmax_block(s0, s1, m, l);
-            const bf16x8_t pb = p_operand(s0, s1);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int dm = 0; dm < 8; ++dm) {
-                acc[dm] *= alpha;
-                acc[dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand(vs, dm, n, g), pb, acc[dm], 0, 0, 0);
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            cur = nxt;
+        const int stride = 4 * BLK;
+        const int nblk = (end - first + stride - 1) / stride;
+        auto sub = [&](int blk) { return (owner && blk <= pos && pos < blk + BLK) ? pos - blk : -1; };
+        // Every load inside the loop is unconditional and the last one or two
+        // blocks are peeled: the compiler's wait counting, which merges
+        // control-flow paths conservatively, then waits for exactly the set
+        // about to be used and leaves the other in flight.
+        int it = 0;
+        for (; it + 2 < nblk; it += 2) {
+            const int b0 = first + it * stride, b1 = b0 + stride;
+            load_kv(rb, kbase, vbase, b1, end - 1, lane);
+            decode_block(st, ra, kt, vt, b0, end, sub(b0), knew, vnew, a.scale, lane);
+            load_kv(ra, kbase, vbase, b1 + stride, end - 1, lane);
+            decode_block(st, rb, kt, vt, b1, end, sub(b1), knew, vnew, a.scale, lane);
+        }
+        const int b0 = first + it * stride;
+        if (it + 1 < nblk) {
+            load_kv(rb, kbase, vbase, b0 + stride, end - 1, lane);
+            decode_block(st, ra, kt, vt, b0, end, sub(b0), knew, vnew, a.scale, lane);
+            decode_block(st, rb, kt, vt, b0 + stride, end, sub(b0 + stride), knew, vnew, a.scale, lane);
+        } else {
+            decode_block(st, ra, kt, vt, b0, end, sub(b0), knew, vnew, a.scale, lane);
         }
     }
 
-    // Merge the four waves (lane n < 4 holds head n: O^T[16dm + 4g + i][n]).
+    // Merge the four waves (lane n < 4 holds head n: O^T[16dm + 4g + i][n]);
+    // each wave parks its accumulator in its own K tile.
+    float* macc = reinterpret_cast<float*>(tiles[0][0]);  // [4 waves][GROUP][D], wave w inside tiles[w]
+    constexpr int WSTRIDE = 2 * BLK * D / 2;              // floats per wave region
     if (n < GROUP) {
-        if (g == 0) { mm[w][n] = m; ll[w][n] = l; }
+        if (g == 0) { mm[w][n] = st.m; ll[w][n] = st.l; }
 #pragma unroll
         for (int dm = 0; dm < 8; ++dm)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) macc[w][n][16 * dm + 4 * g + i] = acc[dm][i];
+            for (int i = 0; i < 4; ++i) macc[w * WSTRIDE + n * D + 16 * dm + 4 * g + i] = st.acc[dm][i];
     }
     __syncthreads();
     for (int e = tid; e < GROUP * D; e += THREADS) {
@@ -306,7 +354,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
         for (int ww = 0; ww < 4; ++ww) {
             if (ll[ww][h] > 0.f) {
                 const float wt = expf(mm[ww][h] - M);
-                sacc += macc[ww][h][d] * wt;
+                sacc += macc[ww * WSTRIDE + h * D + d] * wt;
                 sl += ll[ww][h] * wt;
             }
         }
@@ -318,43 +366,6 @@ __global__ __launch_bounds__(THREADS) void attn_decode_kernel(DecodeArgs a) {
             a.part_ml[2 * p + 1] = sl;
         }
     }
-    if (a.out == nullptr) return;
-
-    // Log-sum-exp merge of the splits by the last workgroup of this (b, kvh)
-    // (reference fused.py:793-823).  The others exit; nothing waits.
-    __syncthreads();
-    int* cnt = a.counter + b * a.Hkv + kvh;
-    if (tid == 0) {
-        __threadfence();
-        const int prev = atomicAdd(cnt, 1);
-        s_last = (prev == a.splits - 1);
-        __threadfence();
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int e = tid; e < GROUP * D; e += THREADS) {
-        const int h = e / D, d = e % D;
-        const int qh = kvh * GROUP + h;
-        const int64_t base = ((int64_t)b * a.Hq + qh) * a.splits;
-        float M = -INFINITY;
-        for (int sp = 0; sp < a.splits; ++sp) {
-            const float* ml = a.part_ml + 2 * (base + sp);
-            if (__builtin_nontemporal_load(ml + 1) > 0.f) M = fmaxf(M, __builtin_nontemporal_load(ml));
-        }
-        float sacc = 0.f, tot = 0.f;
-        for (int sp = 0; sp < a.splits; ++sp) {
-            const float* ml = a.part_ml + 2 * (base + sp);
-            const float ls = __builtin_nontemporal_load(ml + 1);
-            if (ls > 0.f) {
-                const float wt = expf(__builtin_nontemporal_load(ml) - M);
-                sacc += __builtin_nontemporal_load(a.part_acc + (base + sp) * D + d) * wt;
-                tot += ls * wt;
-            }
-        }
-        a.out[((int64_t)b * a.Hq + qh) * D + d] = (bf16_t)f2bf(tot > 0.f ? sacc / tot : 0.f);
-    }
-    if (tid == 0) *cnt = 0;  // ready for the next launch
 }
 
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
@@ -522,25 +533,29 @@ __global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, 
 }  // namespace
 
 extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
-    int per = 256;
-    if ((long)B * Hkv * ((capacity + 255) / 256) < 512) per = 128;
-    int s = (capacity + per - 1) / per;
-    return s < 1 ? 1 : s;
+    // About 1024 workgroups (two resident per CU, two rounds) with at least
+    // 256 keys (two blocks per wave) per split; when even that leaves CUs idle
+    // (short contexts at small batch), 128 keys per split to spread the
+    // latency-bound work.
+    const long heads = (long)B * Hkv;
+    const long want = (1024 + heads - 1) / heads;
+    long most = (capacity + 255) / 256;
+    if (heads * most < 256) most = (capacity + 127) / 128;
+    const long s = want < most ? want : most;
+    return s < 1 ? 1 : (int)s;
 }
 
 extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const bf16_t* q_norm_w,
                               const bf16_t* k_norm_w, const bf16_t* cos_table,
                               const bf16_t* sin_table, const int64_t* pos,
                               bf16_t* cache_k, bf16_t* cache_v, float* part_acc, float* part_ml,
-                              bf16_t* out, int* counter,
                               int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                               hipStream_t stream) {
     if (B < 1 || Hkv < 1 || Hq != GROUP * Hkv || capacity < 1 || splits < 1 || ld_qkv < (Hq + 2 * Hkv) * D)
         return (int)hipErrorInvalidValue;
-    if (!qkv || !pos || !cache_k || !cache_v || !part_acc || !part_ml || (out && !counter))
-        return (int)hipErrorInvalidValue;
+    if (!qkv || !pos || !cache_k || !cache_v || !part_acc || !part_ml) return (int)hipErrorInvalidValue;
     DecodeArgs a{qkv, ld_qkv, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
-                 part_acc, part_ml, out, counter, Hq, Hkv, capacity, splits, eps, scale};
+                 part_acc, part_ml, Hq, Hkv, capacity, splits, eps, scale};
     hipLaunchKernelGGL(attn_decode_kernel, dim3(splits, Hkv, B), dim3(THREADS), 0, stream, a);
     Q3_CHECK_LAUNCH();
 }

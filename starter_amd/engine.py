@@ -322,7 +322,7 @@ class Engine:
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
             call("q3_attn_decode", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml), None, None,
+                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
                  B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
             call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
             if self.small:
