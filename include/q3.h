@@ -80,6 +80,18 @@ int q3_skinny(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K
  * instruction reads 1 KB of contiguous weights. */
 int q3_skinny_tiled(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
                     int epi, uint16_t *y, int ldy, float *ws, hipStream_t stream);
+/* q3_skinny_tiled without an epilogue: the FP32 split partials
+ * ws [q3_skinny_splits(M, N, K), M, N] (one split included), for consumers
+ * that sum them in split order: q3_add_rmsnorm_partials, q3_attn_decode. */
+int q3_skinny_partials(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
+                       float *ws, hipStream_t stream);
+/* LM head + greedy choice for 1..64 rows on tiled weights (shapes with one
+ * split, i.e. wide N): per-workgroup maxima of the BF16 logits, lowest index on
+ * ties, into part_val/part_idx [N/64, M] for q3_argmax_finish (nparts = N/64);
+ * logits [M, ld_logits] are stored too when non-NULL.  engine/engine.py:833. */
+int q3_skinny_argmax(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
+                     uint16_t *logits, int ld_logits, float *part_val, int *part_idx,
+                     hipStream_t stream);
 /* Repack row-major W [N, K] (N % 16 == 0, K % 32 == 0) into 16-row tiles:
  * element (n, k) goes to ((n/16 * K/32 + k/32) * 64 + (k%32)/8 * 16 + n%16) * 8
  * + k%8, the MFMA A-operand order of one wave.  Setup-time layout change for
@@ -93,6 +105,13 @@ int q3_skinny_ws_floats(int M, int N, int K);
  * (rmsnorm.py:48, engine.py:75).  cols % 8 == 0. */
 int q3_rmsnorm(const uint16_t *x, int ldx, const uint16_t *w, uint16_t *y, int ldy,
                int rows, int cols, float eps, hipStream_t stream);
+
+/* resid = bf16(resid + bf16(sum of the split partials ws [splits, rows, cols]
+ * in split order)); y = RMSNorm(resid).  A split-K projection's residual
+ * epilogue fused with the next add_norm (fused.py:147, 525-550).
+ * cols % 8 == 0, cols <= 4096, splits <= 16. */
+int q3_add_rmsnorm_partials(const float *ws, int splits, uint16_t *resid, const uint16_t *w,
+                            uint16_t *y, int rows, int cols, float eps, hipStream_t stream);
 
 /* sum = bf16(res + delta); y = RMSNorm(sum).  add_norm (fused.py:147).
  * sum_out may equal res (in place). */
@@ -120,12 +139,16 @@ int q3_qk_norm_rope_kv(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w
 
 /* Split-K GQA decode attention for the token at position *pos (one query per
  * sequence), with the q/k RMSNorm + RoPE and the KV append of that token fused
- * in.  qkv [B, ld_qkv] (q | k | v); cache_k/v [B, Hkv, capacity, 128].
+ * in.  qkv [B, ld_qkv] (q | k | v), or, when qkv_part != NULL (qkv unused),
+ * the projection's FP32 split partials [qkv_splits, B, ld_qkv] from
+ * q3_skinny_partials, summed in split order and rounded to BF16;
+ * cache_k/v [B, Hkv, capacity, 128].
  * Writes per-split partials part_acc [B, Hq, splits, 128] (FP32, unnormalised)
  * and part_ml [B, Hq, splits, 2] (running max, sum); q3_attn_merge finishes.
  * Any splits >= 1 is valid; q3_attn_splits gives the tuned count.
  * decode_attention_gqa / _split (fused.py:641-846). */
-int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w,
+int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
+                   const uint16_t *q_norm_w,
                    const uint16_t *k_norm_w, const uint16_t *cos_table,
                    const uint16_t *sin_table, const int64_t *pos,
                    uint16_t *cache_k, uint16_t *cache_v, float *part_acc, float *part_ml,

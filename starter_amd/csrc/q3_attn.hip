@@ -130,6 +130,8 @@ __device__ __forceinline__ void norm_rope_pair(float lo, float hi, const bf16_t*
 struct DecodeArgs {
     const bf16_t* qkv;
     int ld_qkv;
+    const float* qkv_part;  // optional: FP32 split partials [qkv_splits, B, ld_qkv] instead of qkv
+    int qkv_splits;
     const bf16_t* q_norm_w;
     const bf16_t* k_norm_w;
     const bf16_t* cos_t;
@@ -142,6 +144,39 @@ struct DecodeArgs {
     int Hq, Hkv, capacity, splits;
     float eps, scale;
 };
+
+// Elements idx and idx + 64 of sequence b's projected q|k|v row: BF16 from
+// qkv, or the split partials summed in split order and rounded to BF16 (the
+// value the projection's own STORE epilogue would have written).  Splits are
+// read four at a time with every load of a group issued before the sums.
+__device__ __forceinline__ void qkv_pair(const DecodeArgs& a, int b, int idx, float& lo, float& hi) {
+    if (a.qkv_part == nullptr) {
+        const bf16_t* r = a.qkv + (int64_t)b * a.ld_qkv + idx;
+        lo = bf2f(r[0]);
+        hi = bf2f(r[64]);
+        return;
+    }
+    const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;  // one split: [B, ld_qkv]
+    const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
+    float slo = 0.f, shi = 0.f;
+    for (int s0 = 0; s0 < a.qkv_splits; s0 += 4) {
+        float l4[4], h4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t o = (int64_t)min(s0 + j, a.qkv_splits - 1) * stride;
+            l4[j] = base[o];
+            h4[j] = base[o + 64];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (s0 + j < a.qkv_splits) {
+                slo += l4[j];
+                shi += h4[j];
+            }
+    }
+    lo = rbf(slo);
+    hi = rbf(shi);
+}
 
 // One 32-key block of K and V rows in registers: load j covers keys 4j..4j+3
 // whole, lane l holding chunk (l % 16) ^ (key & 15) of key 4j + l / 16, which is
@@ -247,11 +282,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
 
     // Everything that does not depend on the position is requested first.
     const int pos_raw = (int)*a.pos;
-    const bf16_t* row = a.qkv + (int64_t)b * a.ld_qkv;
-    const bf16_t* qrow = row + (kvh * GROUP + w) * D;
-    const float q_lo = bf2f(qrow[lane]), q_hi = bf2f(qrow[lane + 64]);
-    const bf16_t* krow = row + a.Hq * D + kvh * D;
-    const bf16_t* vrow = row + (a.Hq + a.Hkv) * D + kvh * D;
+    float q_lo, q_hi;
+    qkv_pair(a, b, (kvh * GROUP + w) * D + lane, q_lo, q_hi);
     KVRegs ra, rb;
     const int first = begin + w * BLK;
     if (first < range_end) load_kv(ra, kbase, vbase, first, range_end - 1, lane);
@@ -272,7 +304,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
         qs[w][lane + 64] = (bf16_t)hi;
         if (owner && w == 0) {
             // This token's key: normalised, rotated, appended (fused.py:553-617).
-            norm_rope_pair(bf2f(krow[lane]), bf2f(krow[lane + 64]), a.k_norm_w, cosr, sinr, a.eps, lane, lo, hi);
+            float k_lo, k_hi;
+            qkv_pair(a, b, a.Hq * D + kvh * D + lane, k_lo, k_hi);
+            norm_rope_pair(k_lo, k_hi, a.k_norm_w, cosr, sinr, a.eps, lane, lo, hi);
             knew[lane] = (bf16_t)lo;
             knew[lane + 64] = (bf16_t)hi;
             bf16_t* dst = a.cache_k + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
@@ -280,7 +314,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
             dst[lane + 64] = (bf16_t)hi;
         }
         if (owner && w == 1) {
-            const bf16_t v0 = vrow[lane], v1 = vrow[lane + 64];
+            float v_lo, v_hi;
+            qkv_pair(a, b, (a.Hq + a.Hkv) * D + kvh * D + lane, v_lo, v_hi);
+            const bf16_t v0 = (bf16_t)f2bf(v_lo), v1 = (bf16_t)f2bf(v_hi);
             vnew[lane] = v0;
             vnew[lane + 64] = v1;
             bf16_t* dst = a.cache_v + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
@@ -545,7 +581,8 @@ extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     return s < 1 ? 1 : (int)s;
 }
 
-extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const bf16_t* q_norm_w,
+extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_part, int qkv_splits,
+                              const bf16_t* q_norm_w,
                               const bf16_t* k_norm_w, const bf16_t* cos_table,
                               const bf16_t* sin_table, const int64_t* pos,
                               bf16_t* cache_k, bf16_t* cache_v, float* part_acc, float* part_ml,
@@ -553,8 +590,10 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const bf16_t* q_nor
                               hipStream_t stream) {
     if (B < 1 || Hkv < 1 || Hq != GROUP * Hkv || capacity < 1 || splits < 1 || ld_qkv < (Hq + 2 * Hkv) * D)
         return (int)hipErrorInvalidValue;
-    if (!qkv || !pos || !cache_k || !cache_v || !part_acc || !part_ml) return (int)hipErrorInvalidValue;
-    DecodeArgs a{qkv, ld_qkv, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
+    if ((!qkv && !qkv_part) || (qkv_part && (qkv_splits < 1 || (reinterpret_cast<uintptr_t>(qkv_part) & 3))) ||
+        !pos || !cache_k || !cache_v || !part_acc || !part_ml)
+        return (int)hipErrorInvalidValue;
+    DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
                  part_acc, part_ml, Hq, Hkv, capacity, splits, eps, scale};
     hipLaunchKernelGGL(attn_decode_kernel, dim3(splits, Hkv, B), dim3(THREADS), 0, stream, a);
     Q3_CHECK_LAUNCH();

@@ -13,6 +13,8 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int MAX_CHUNKS = 4;  // 16-byte chunks per thread kept in registers (cols <= 8192)
+constexpr int PARTIAL_CHUNKS = 2;  // the same for the split-partial sum (cols <= 4096)
+constexpr int MAX_PARTIAL_SPLITS = 16;
 
 // Block-wide sum (256 threads).
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -85,6 +87,62 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(const bf16_t* a, int l
         if (c < chunks) {
             const uint4 g = *reinterpret_cast<const uint4*>(w + c * 8);
             *reinterpret_cast<uint4*>(y + (int64_t)row * ldy + c * 8) = norm8(xv[j], g, inv);
+        }
+    }
+}
+
+// resid[row] = bf16(resid + bf16(sum_s ws[s][row])) (splits summed in order, as
+// the projection's own reduce does), then y = RMSNorm(resid[row]) with the
+// same per-thread chunking and block sum as rmsnorm_kernel: the fused result
+// is bit-identical to the projection's RESID epilogue followed by q3_rmsnorm.
+// Every split's load for a chunk is issued before the sum (indices past the
+// count re-read the last split and are masked).
+template <int MAXS>
+__global__ __launch_bounds__(THREADS) void add_rmsnorm_partials_kernel(const float* ws, int splits, int rows,
+                                                                       bf16_t* resid, const bf16_t* w, bf16_t* y,
+                                                                       int cols, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int chunks = cols >> 3;
+    bf16_t* rrow = resid + (int64_t)row * cols;
+    uint4 xv[PARTIAL_CHUNKS];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
+        const int c = threadIdx.x + j * THREADS;
+        if (c < chunks) {
+            f32x4_t lo[MAXS], hi[MAXS];
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s) {
+                const float* src = ws + ((int64_t)min(s, splits - 1) * rows + row) * cols + c * 8;
+                lo[s] = *reinterpret_cast<const f32x4_t*>(src);
+                hi[s] = *reinterpret_cast<const f32x4_t*>(src + 4);
+            }
+            f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s)
+                if (s < splits) {
+                    a += lo[s];
+                    b += hi[s];
+                }
+            const uint4 r = *reinterpret_cast<const uint4*>(rrow + c * 8);
+            uint4 v;
+            v.x = pack2(f2bf(bflo(r.x) + rbf(a[0])), f2bf(bfhi(r.x) + rbf(a[1])));
+            v.y = pack2(f2bf(bflo(r.y) + rbf(a[2])), f2bf(bfhi(r.y) + rbf(a[3])));
+            v.z = pack2(f2bf(bflo(r.z) + rbf(b[0])), f2bf(bfhi(r.z) + rbf(b[1])));
+            v.w = pack2(f2bf(bflo(r.w) + rbf(b[2])), f2bf(bfhi(r.w) + rbf(b[3])));
+            *reinterpret_cast<uint4*>(rrow + c * 8) = v;
+            xv[j] = v;
+            ss += sumsq8(v);
+        }
+    }
+    const float inv = inv_rms(block_sum(ss, red), cols, eps);
+#pragma unroll
+    for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
+        const int c = threadIdx.x + j * THREADS;
+        if (c < chunks) {
+            const uint4 g = *reinterpret_cast<const uint4*>(w + c * 8);
+            *reinterpret_cast<uint4*>(y + (int64_t)row * cols + c * 8) = norm8(xv[j], g, inv);
         }
     }
 }
@@ -226,6 +284,23 @@ extern "C" int q3_add_rmsnorm(const bf16_t* res, const bf16_t* delta, bf16_t* su
         return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel<SRC_ADD>, dim3(rows), dim3(THREADS), 0, stream, res, cols, delta,
                        nullptr, sum_out, w, y, cols, cols, eps);
+    Q3_CHECK_LAUNCH();
+}
+
+extern "C" int q3_add_rmsnorm_partials(const float* ws, int splits, bf16_t* resid, const bf16_t* w, bf16_t* y,
+                                       int rows, int cols, float eps, hipStream_t stream) {
+    if (rows < 1 || cols < 8 || cols % 8 || cols > PARTIAL_CHUNKS * THREADS * 8 || splits < 1 ||
+        splits > MAX_PARTIAL_SPLITS || !ws || !aligned16(ws) || !aligned16(resid) || !aligned16(y) || !aligned16(w))
+        return (int)hipErrorInvalidValue;
+    if (splits <= 4)
+        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<4>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
+                           resid, w, y, cols, eps);
+    else if (splits <= 8)
+        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<8>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
+                           resid, w, y, cols, eps);
+    else
+        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<MAX_PARTIAL_SPLITS>, dim3(rows), dim3(THREADS), 0, stream, ws,
+                           splits, rows, resid, w, y, cols, eps);
     Q3_CHECK_LAUNCH();
 }
 

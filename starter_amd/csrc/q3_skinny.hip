@@ -39,7 +39,10 @@ struct SkinnyArgs {
     int epi;
     bf16_t* y;
     int ldy;
-    float* ws;                  // [splits, M, N] FP32 partials when splits > 1
+    float* ws;                  // [splits, M, N] FP32 partials when splits > 1 or part_only
+    bool part_only;             // write the partials even with one split, no epilogue
+    float* part_val;            // argmax epilogues: [N/64, M] per-workgroup maxima
+    int* part_idx;              //   and their rows (first on ties)
 };
 
 template <int MT>
@@ -80,6 +83,57 @@ __device__ __forceinline__ void load_w_tiled(const bf16_t* wtile, int k0, int la
     for (int j = 0; j < 8; ++j) wr[j] = load_nt(wtile + (int64_t)(k0 / 32 + j) * 512 + lane * 8);
 }
 
+// Greedy-token epilogue (one split, N % 64 == 0 so every wave is active): the
+// BF16-rounded logit maximum of this workgroup's 64 rows for each batch row,
+// lowest row on ties (reference engine/engine.py:833 torch.argmax), into
+// part_val/part_idx [N/64, M]; STORE_ARGMAX also stores the logits.  red is
+// LDS scratch for 2 * 4 * 16 * MT words (the x tile, free by now).
+template <int MT>
+__device__ __forceinline__ void argmax_epilogue(const SkinnyArgs& a, const f32x4_t (&acc)[MT], int row0, int wave,
+                                                int lane, float* red) {
+    const int g = lane >> 4, n = lane & 15;
+    float* rv = red;
+    int* ri = reinterpret_cast<int*>(red + 4 * 16 * MT);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + n;
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t bits = f2bf(acc[t][i]);
+            const float v = bf2f((bf16_t)bits);
+            const int r = row0 + 4 * g + i;
+            if (a.epi == Q3_EPI_STORE_ARGMAX && m < a.M) a.y[(int64_t)m * a.ldy + r] = (bf16_t)bits;
+            if (v > bv || (v == bv && r < bi)) { bv = v; bi = r; }
+        }
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+            const float ov = __shfl_xor(bv, off, Q3_WAVE);
+            const int oi = __shfl_xor(bi, off, Q3_WAVE);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (g == 0) {
+            rv[wave * 16 * MT + m] = bv;
+            ri[wave * 16 * MT + m] = bi;
+        }
+    }
+    __syncthreads();
+    const int m = threadIdx.x;
+    if (m < a.M) {
+        float bv = rv[m];
+        int bi = ri[m];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float ov = rv[w * 16 * MT + m];
+            const int oi = ri[w * 16 * MT + m];
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        a.part_val[(int64_t)blockIdx.x * a.M + m] = bv;
+        a.part_idx[(int64_t)blockIdx.x * a.M + m] = bi;
+    }
+}
+
 // NCH chunks per split, fully unrolled: weight loads run two chunks ahead in a
 // three-slot register ring, x one chunk ahead through a double-buffered LDS
 // tile.  Loads are issued x(c+1) then W(c+2), so storing x(c+1) waits only for
@@ -103,7 +157,7 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
     };
     if (kbeg >= a.K) {
         // A split past the end of K contributes zeros (uniform exit: no barrier pending).
-        if (a.splits > 1 && active)
+        if ((a.splits > 1 || a.part_only) && active)
             for (int m = n; m < a.M; m += 16)
                 *reinterpret_cast<float4*>(a.ws + ((int64_t)split * a.M + m) * a.N + row0 + 4 * g) =
                     make_float4(0.f, 0.f, 0.f, 0.f);
@@ -145,6 +199,10 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
             __syncthreads();
         }
     }
+    if (a.epi == Q3_EPI_ARGMAX || a.epi == Q3_EPI_STORE_ARGMAX) {
+        argmax_epilogue<MT>(a, acc, row0, wave, lane, reinterpret_cast<float*>(xs));
+        return;
+    }
     if (!active) return;
 
     // acc[t][i] = partial (weight row row0 + 4g + i, batch row 16t + n).
@@ -153,7 +211,7 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
         const int m = 16 * t + n;
         if (m >= a.M) continue;
         const int r = row0 + 4 * g;
-        if (a.splits > 1) {
+        if (a.splits > 1 || a.part_only) {
             float* dst = a.ws + ((int64_t)split * a.M + m) * a.N + r;
             *reinterpret_cast<float4*>(dst) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
         } else if (a.epi == Q3_EPI_SWIGLU) {
@@ -173,18 +231,27 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
 }
 
 // Fixed-order sum of the split partials, then the epilogue.  One thread per
-// (batch row, output pair).
+// (batch row, output pair); every split's load is issued before the sum
+// (split indices past the count re-read the last split and are masked), so the
+// kernel costs one memory round trip, not one per split.
+template <int MAXS>
 __global__ __launch_bounds__(THREADS) void skinny_reduce_kernel(const float* ws, int splits, int M, int N, int epi,
                                                                 bf16_t* y, int ldy) {
     const int64_t e = (int64_t)blockIdx.x * THREADS + threadIdx.x;  // pair index
     const int pairs = N / 2;
     if (e >= (int64_t)M * pairs) return;
     const int m = (int)(e / pairs), c = 2 * (int)(e % pairs);
+    float2 p[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s)
+        p[s] = *reinterpret_cast<const float2*>(ws + ((int64_t)min(s, splits - 1) * M + m) * N + c);
     float v0 = 0.f, v1 = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float2 p = *reinterpret_cast<const float2*>(ws + ((int64_t)s * M + m) * N + c);
-        v0 += p.x;
-        v1 += p.y;
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        if (s < splits) {
+            v0 += p[s].x;
+            v1 += p[s].y;
+        }
     }
     if (epi == Q3_EPI_SWIGLU) {
         y[(int64_t)m * ldy + (c >> 1)] = (bf16_t)f2bf(silu_bf16(rbf(v0)) * rbf(v1));
@@ -276,27 +343,41 @@ extern "C" int q3_skinny_ws_floats(int M, int N, int K) {
 
 namespace {
 
-int skinny_launch(bool tiled, const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
-                  int ldy, float* ws, hipStream_t stream) {
-    if (M < 1 || M > 64 || N < 1 || N % 64 || K < KC || K % KC || ldx % 8 || !x || !w || !y ||
+constexpr int MAX_SPLITS = 16;
+
+int skinny_launch(bool tiled, bool part_only, const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K,
+                  int epi, bf16_t* y, int ldy, float* ws, float* part_val, int* part_idx, hipStream_t stream) {
+    if (M < 1 || M > 64 || N < 1 || N % 64 || K < KC || K % KC || ldx % 8 || !x || !w ||
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15))
         return (int)hipErrorInvalidValue;
-    if (epi != Q3_EPI_STORE && epi != Q3_EPI_RESID && epi != Q3_EPI_SWIGLU) return (int)hipErrorInvalidValue;
+    const bool argmax = epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX;
+    if (epi != Q3_EPI_STORE && epi != Q3_EPI_RESID && epi != Q3_EPI_SWIGLU && !argmax)
+        return (int)hipErrorInvalidValue;
     const int splits = q3_skinny_splits(M, N, K);
-    if (splits > 1 && !ws) return (int)hipErrorInvalidValue;
+    if (splits > MAX_SPLITS) return (int)hipErrorInvalidValue;
+    if (argmax && (splits != 1 || !part_val || !part_idx || (epi == Q3_EPI_STORE_ARGMAX && !y)))
+        return (int)hipErrorInvalidValue;
+    if (!argmax && !part_only && !y) return (int)hipErrorInvalidValue;
+    if ((splits > 1 || part_only) && !ws) return (int)hipErrorInvalidValue;
     const int chunks = K / KC;
     const int kper = (chunks + splits - 1) / splits * KC;
-    SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws};
+    SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws, part_only, part_val, part_idx};
     const dim3 grid(N / ROWS, splits);
     const int mt = (M + 15) / 16;
     const int nch = kper / KC;
     const int bad = tiled ? launch_mt<true>(mt, nch, grid, a, stream) : launch_mt<false>(mt, nch, grid, a, stream);
     if (bad) return (int)hipErrorInvalidValue;
     hipError_t rc = hipGetLastError();
-    if (rc != hipSuccess || splits == 1) return (int)rc;
+    if (rc != hipSuccess || splits == 1 || part_only) return (int)rc;
     const int64_t pairs = (int64_t)M * (N / 2);
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((pairs + THREADS - 1) / THREADS)), dim3(THREADS), 0,
-                       stream, ws, splits, M, N, epi, y, ldy);
+    const dim3 rgrid((unsigned)((pairs + THREADS - 1) / THREADS));
+    if (splits <= 4)
+        hipLaunchKernelGGL(skinny_reduce_kernel<4>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
+    else if (splits <= 8)
+        hipLaunchKernelGGL(skinny_reduce_kernel<8>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
+    else
+        hipLaunchKernelGGL(skinny_reduce_kernel<MAX_SPLITS>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi,
+                           y, ldy);
     Q3_CHECK_LAUNCH();
 }
 
@@ -304,12 +385,25 @@ int skinny_launch(bool tiled, const bf16_t* x, int ldx, const bf16_t* w, int M, 
 
 extern "C" int q3_skinny(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
                          int ldy, float* ws, hipStream_t stream) {
-    return skinny_launch(false, x, ldx, w, M, N, K, epi, y, ldy, ws, stream);
+    if (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) return (int)hipErrorInvalidValue;
+    return skinny_launch(false, false, x, ldx, w, M, N, K, epi, y, ldy, ws, nullptr, nullptr, stream);
 }
 
 extern "C" int q3_skinny_tiled(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, int epi, bf16_t* y,
                                int ldy, float* ws, hipStream_t stream) {
-    return skinny_launch(true, x, ldx, wt, M, N, K, epi, y, ldy, ws, stream);
+    if (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) return (int)hipErrorInvalidValue;
+    return skinny_launch(true, false, x, ldx, wt, M, N, K, epi, y, ldy, ws, nullptr, nullptr, stream);
+}
+
+extern "C" int q3_skinny_partials(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, float* ws,
+                                  hipStream_t stream) {
+    return skinny_launch(true, true, x, ldx, wt, M, N, K, Q3_EPI_STORE, nullptr, 0, ws, nullptr, nullptr, stream);
+}
+
+extern "C" int q3_skinny_argmax(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, bf16_t* logits,
+                                int ld_logits, float* part_val, int* part_idx, hipStream_t stream) {
+    return skinny_launch(true, false, x, ldx, wt, M, N, K, logits ? Q3_EPI_STORE_ARGMAX : Q3_EPI_ARGMAX, logits,
+                         ld_logits, nullptr, part_val, part_idx, stream);
 }
 
 extern "C" int q3_tile16(const bf16_t* w, int N, int K, bf16_t* out, hipStream_t stream) {

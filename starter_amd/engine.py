@@ -35,7 +35,9 @@ Decode step (one hipGraph, self-feeding like reference ``:805-839``), B <= 8:
   gemv(norm -> qkv of the next layer) ... | gemv(norm -> lm_head -> argmax
   partials) | argmax finish (token -> input buffer, pos += 1).
 For B > GEMV_BATCH_MAX the projections stream 16-row tiled weight copies into
-MFMA (B <= 64) or run on the LDS-tiled MFMA GEMM, with separate norm kernels.
+MFMA (B <= 64), their split-K partials summed by the consuming kernel (the
+attention prologue, the residual add + RMSNorm); above 64 rows, or for shapes
+that do not tile, the LDS-tiled MFMA GEMM with separate norm kernels.
 """
 
 from __future__ import annotations
@@ -245,20 +247,39 @@ class Engine:
         self.part_acc = self._empty(B, self.HEADS, self.splits, D, dtype=torch.float32)
         self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
         self.small = B <= GEMV_BATCH_MAX
-        self.skinny = not self.small and B <= SKINNY_BATCH_MAX
-        # Split-K workspace of the MFMA decode projections.
+        self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
+        # Split-K workspace of the MFMA decode projections: every projection's
+        # partials, [splits, B, N] FP32, one consumer at a time.
         ws = 0
         if self.skinny:
             self._make_tiled()
-            for N, K in ((self.qkv_size, H), (H, self.q_size), (2 * self.INTER, H), (H, self.INTER), (V, H)):
-                ws = max(ws, call("q3_skinny_ws_floats", B, N, K))
+            for N, K in self._projections():
+                ws = max(ws, call("q3_skinny_splits", B, N, K) * B * N)
         self.skinny_ws = self._empty(max(ws, 1), dtype=torch.float32)
         if self.small:
             self.lm_parts = call("q3_gemv_partials", B, V, _lib.EPI_ARGMAX)
+        elif self.skinny:
+            self.lm_parts = V // 64
+        if self.small or self.skinny:
             self.part_val = self._empty(self.lm_parts, B, dtype=torch.float32)
             self.part_idx = self._empty(self.lm_parts, B, dtype=torch.int32)
         self.logits = self._empty(B, V)
         self._capture()
+
+    def _projections(self) -> list[tuple[int, int]]:
+        """(N, K) of qkv, o, gate_up, down and the LM head."""
+        H = self.HIDDEN
+        return [(self.qkv_size, H), (H, self.q_size), (2 * self.INTER, H), (H, self.INTER), (self.VOCAB, H)]
+
+    def _skinny_shapes_ok(self, B: int) -> bool:
+        """The fused MFMA decode path needs every projection to tile (N % 64,
+        K % 256, at most 16 splits), the LM head unsplit, hidden <= 4096."""
+        if self.HIDDEN > 4096:
+            return False
+        for N, K in self._projections():
+            if N % 64 or K % 256 or call("q3_skinny_splits", B, N, K) > 16:
+                return False
+        return call("q3_skinny_splits", B, self.VOCAB, self.HIDDEN) == 1
 
     def _make_tiled(self) -> None:
         """16-row tiled copies of every decode weight (``q3_tile16``), kept for the
@@ -295,6 +316,9 @@ class Engine:
 
     def _enqueue_decode(self) -> None:
         """One self-feeding decode step on ``self.stream`` (reference ``_forward_decode``)."""
+        if self.skinny:
+            self._enqueue_decode_skinny()
+            return
         s = self._s
         B, H, I, V = self.batch, self.HIDDEN, self.INTER, self.VOCAB
         D, Hq, Hkv, C = self.HEAD_DIM, self.HEADS, self.KV_HEADS, self.capacity
@@ -320,7 +344,7 @@ class Engine:
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
-            call("q3_attn_decode", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
+            call("q3_attn_decode", qkv, self.qkv_size, None, 0, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
                  vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
                  B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
@@ -348,15 +372,47 @@ class Engine:
             self._proj(nbuf, H, self.lm_head, V, H, _lib.EPI_STORE, _ptr(self.logits), V)
             call("q3_argmax_rows", _ptr(self.logits), V, B, V, tok, pos, s)
 
+    def _enqueue_decode_skinny(self) -> None:
+        """Decode step for 5..64 rows: tiled-weight MFMA projections whose split-K
+        partials go straight to their consumers -- qkv into the attention
+        prologue, o and down into the residual add + next RMSNorm -- so a layer is
+        seven or eight kernels (reference ``engine/engine.py:805-839`` runs the
+        same math as separate ops)."""
+        s = self._s
+        B, H, I, V = self.batch, self.HIDDEN, self.INTER, self.VOCAB
+        Hq, Hkv, C = self.HEADS, self.KV_HEADS, self.capacity
+        layer_stride = self.cache_k[0].numel() * 2
+        kc0, vc0 = self.cache_k.data_ptr(), self.cache_v.data_ptr()
+        tok, pos = _ptr(self.g_token), _ptr(self.g_pos)
+        resid, attn, act, nbuf, ws = (_ptr(self.resid), _ptr(self.attn_out), _ptr(self.act), _ptr(self.nbuf),
+                                      _ptr(self.skinny_ws))
+        T = lambda w: _ptr(self.tiled[id(w)])  # noqa: E731
+        s_qkv = call("q3_skinny_splits", B, self.qkv_size, H)
+        s_o = call("q3_skinny_splits", B, H, self.q_size)
+        s_down = call("q3_skinny_splits", B, H, I)
+        call("q3_embed_rmsnorm", tok, _ptr(self.embed), resid, nbuf, _ptr(self.layers[0]["in_ln"]), B, H,
+             self.EPS, s)
+        for i, L in enumerate(self.layers):
+            call("q3_skinny_partials", nbuf, H, T(L["qkv"]), B, self.qkv_size, H, ws, s)
+            call("q3_attn_decode", None, self.qkv_size, ws, s_qkv, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
+                 _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
+                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
+                 B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
+            call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+            call("q3_skinny_partials", attn, self.q_size, T(L["o"]), B, H, self.q_size, ws, s)
+            call("q3_add_rmsnorm_partials", ws, s_o, resid, _ptr(L["post_ln"]), nbuf, B, H, self.EPS, s)
+            call("q3_skinny_tiled", nbuf, H, T(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, ws, s)
+            call("q3_skinny_partials", act, I, T(L["down"]), B, H, I, ws, s)
+            nxt = self.layers[i + 1]["in_ln"] if i + 1 < self.LAYERS else self.final_norm
+            call("q3_add_rmsnorm_partials", ws, s_down, resid, _ptr(nxt), nbuf, B, H, self.EPS, s)
+        call("q3_skinny_argmax", nbuf, H, T(self.lm_head), B, V, H, _ptr(self.logits) if self.keep_logits else None,
+             V, _ptr(self.part_val), _ptr(self.part_idx), s)
+        call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
+
     def _proj(self, x: int, ldx: int, w: torch.Tensor, N: int, K: int, epi: int, y: int, ldy: int) -> None:
-        """Decode projection above GEMV_BATCH_MAX: the weight-streaming MFMA kernel on
-        the tiled copy where the shape tiles (N % 64, K % 256) and B <= 64, the
-        LDS-tiled MFMA GEMM otherwise."""
-        if self.skinny and N % 64 == 0 and K % 256 == 0:
-            call("q3_skinny_tiled", x, ldx, _ptr(self.tiled[id(w)]), self.batch, N, K, epi, y, ldy,
-                 _ptr(self.skinny_ws), self._s)
-        else:
-            call("q3_gemm", x, ldx, _ptr(w), self.batch, N, K, epi, y, ldy, self._s)
+        """Decode projection for batches outside the GEMV and fused MFMA paths (more
+        than 64 rows, or shapes that do not tile): the LDS-tiled MFMA GEMM."""
+        call("q3_gemm", x, ldx, _ptr(w), self.batch, N, K, epi, y, ldy, self._s)
 
     def _capture(self) -> None:
         """Warm every kernel eagerly, then record one decode step as a hipGraph.

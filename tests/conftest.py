@@ -37,6 +37,20 @@ def tiny_ckpt(tmp_path_factory):
 
 
 @pytest.fixture(scope="session")
+def tile_ckpt(tmp_path_factory):
+    """A small seeded model whose projections all tile for the fused MFMA decode
+    path (N % 64, K % 256): hidden 512, intermediate 1024, 8/2 heads, vocab 1024."""
+    from starter_amd.checkpoint import Qwen3Config, write_seeded_checkpoint
+
+    cfg = Qwen3Config(num_hidden_layers=2, hidden_size=512, intermediate_size=1024,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                      vocab_size=1024, max_position_embeddings=2048)
+    path = tmp_path_factory.mktemp("tile")
+    write_seeded_checkpoint(path, cfg, 5, 0.05, 0.1)
+    return path
+
+
+@pytest.fixture(scope="session")
 def full_ckpt():
     """The seeded Qwen3-4B checkpoint (8 GB), written once per machine."""
     from starter_amd.checkpoint import ensure_seeded_checkpoint

@@ -55,7 +55,7 @@ def test_bad_arguments_raise_without_launching():
     with pytest.raises(RuntimeError, match="q3_gemm failed"):
         _lib.call("q3_gemm", None, 0, None, 4, 4, 60, 0, None, 0, None)
     with pytest.raises(RuntimeError, match="q3_attn_decode failed"):
-        _lib.call("q3_attn_decode", None, 0, None, None, None, None, None, None, None, None, None,
+        _lib.call("q3_attn_decode", None, 0, None, 0, None, None, None, None, None, None, None, None, None,
                   1, 32, 7, 64, 1, 1e-6, 0.1, None)
 
 

@@ -117,6 +117,26 @@ def test_large_batch_path_matches_oracle(tiny_engine, tiny_ckpt, batch):
     check_stream(steps, logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
 
 
+@pytest.fixture(scope="module")
+def tile_engine(tile_ckpt):
+    return engine_mod.Engine(str(tile_ckpt))
+
+
+@pytest.mark.parametrize("batch", [3, 5, 16, 64])
+def test_fused_mfma_decode_matches_oracle(tile_engine, tile_ckpt, batch):
+    """5..64 rows take the tiled-weight MFMA path with split partials summed by their
+    consumers; 3 rows the GEMVs.  Rows are checked against the CPU oracle."""
+    cfg, tensors = load_checkpoint(tile_ckpt)
+    orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
+    rng = np.random.Generator(np.random.PCG64(100 + batch))
+    ids = rng.integers(0, cfg.vocab_size, (batch, 19)).tolist()
+    want, want_logits = orc.generate(ids, 6, keep_logits=True)
+    steps, logits = tile_engine.trace_logits(ids, 6)
+    assert tile_engine.skinny == (batch > engine_mod.GEMV_BATCH_MAX)
+    check_stream(steps, logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
+    assert list(tile_engine.generate(ids, 6)) == steps
+
+
 def test_batch_rows_are_independent(tiny_engine):
     """A row's tokens do not depend on the other rows of the batch (bit-identical)."""
     rng = np.random.Generator(np.random.PCG64(3))

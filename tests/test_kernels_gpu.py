@@ -321,12 +321,12 @@ def test_attn_decode(B, C, pos, splits):
     out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
     posd = torch.tensor([pos], dtype=torch.int64, device=DEV)
     qkvd, qwd, kwd, cosd, sind = dv(qkv), dv(qw), dv(kw), dv(cos), dv(sin)
-    call("q3_attn_decode", P(qkvd), width, P(qwd), P(kwd), P(cosd), P(sind),
+    call("q3_attn_decode", P(qkvd), width, None, 0, P(qwd), P(kwd), P(cosd), P(sind),
          P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
     # A second call (the row at pos now already holds the new key): same bits.
     again = torch.empty_like(out)
-    call("q3_attn_decode", P(qkvd), width, P(qwd), P(kwd), P(cosd), P(sind),
+    call("q3_attn_decode", P(qkvd), width, None, 0, P(qwd), P(kwd), P(cosd), P(sind),
          P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(again), B, Hq, splits, S())
     torch.cuda.synchronize()
@@ -410,7 +410,8 @@ def test_skinny(M, N, K):
     """Weight-streaming MFMA projection (split-K + fixed-order reduce on narrow N)."""
     x, w = rnd((M, K), 1.0, M + 7), rnd((N, K), 0.02, N + K + 7)
     xd, wd = dv(x), dv(w)
-    ws = torch.empty(max(1, call("q3_skinny_ws_floats", M, N, K)), dtype=torch.float32, device=DEV)
+    splits = call("q3_skinny_splits", M, N, K)
+    ws = torch.empty(splits * M * N, dtype=torch.float32, device=DEV)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     call("q3_skinny", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(y), N, P(ws), S())
     torch.cuda.synchronize()
@@ -422,6 +423,14 @@ def test_skinny(M, N, K):
     call("q3_skinny_tiled", P(xd), K, P(wt), M, N, K, _lib.EPI_STORE, P(yt), N, P(ws), S())
     torch.cuda.synchronize()
     assert torch.equal(yt, y)
+    # Partials only: summed in split order they round to the same bits.
+    call("q3_skinny_partials", P(xd), K, P(wt), M, N, K, P(ws), S())
+    torch.cuda.synchronize()
+    part = ws.view(splits, M, N).cpu()
+    acc = part[0].clone()
+    for sp in range(1, splits):
+        acc += part[sp]
+    assert torch.equal(acc.to(torch.bfloat16), y.cpu())
     res = rnd((M, N), 1.0, 9)
     resd = dv(res)
     call("q3_skinny", P(xd), K, P(wd), M, N, K, _lib.EPI_RESID, P(resd), N, P(ws), S())
@@ -431,3 +440,89 @@ def test_skinny(M, N, K):
     yc = y.cpu()
     assert torch.equal(resd.cpu(), res + yc)
     assert_nearly_exact(act, oc.swiglu(yc[:, 0::2], yc[:, 1::2]), frac=5e-3)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 33, 64])
+@pytest.mark.parametrize("N,K", [(1024, 512), (151936, 256)])
+def test_skinny_argmax(M, N, K):
+    """LM-head epilogue: per-workgroup maxima + q3_argmax_finish = first-index argmax of the BF16 logits."""
+    assert call("q3_skinny_splits", M, N, K) == 1
+    x, w = rnd((M, K), 1.0, M + 3), rnd((N, K), 0.02, 11)
+    # Two identical dominant rows in different workgroups: the lower index must win.
+    w[7] = w[N - 1] = (w[7].float() * 4).to(torch.bfloat16)
+    wt = torch.empty(N, K, dtype=torch.bfloat16, device=DEV)
+    call("q3_tile16", P(dv(w)), N, K, P(wt), S())
+    xd = dv(x)
+    want = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(M * N, dtype=torch.float32, device=DEV)
+    call("q3_skinny_tiled", P(xd), K, P(wt), M, N, K, _lib.EPI_STORE, P(want), N, P(ws), S())
+    parts = N // 64
+    pv = torch.empty(parts, M, dtype=torch.float32, device=DEV)
+    pi = torch.empty(parts, M, dtype=torch.int32, device=DEV)
+    logits = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    for store in (False, True):
+        call("q3_skinny_argmax", P(xd), K, P(wt), M, N, K, P(logits) if store else None, N, P(pv), P(pi), S())
+        call("q3_argmax_finish", P(pv), P(pi), parts, M, P(tok), None, S())
+        torch.cuda.synchronize()
+        ref = want.cpu().float()
+        assert torch.equal(tok.cpu(), ref.argmax(dim=1)), store
+        if store:
+            assert torch.equal(logits.cpu(), want.cpu())
+    assert (ref[:, 7] == ref[:, N - 1]).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 2560, 4096), (16, 2560, 9728), (64, 2560, 9728), (9, 512, 1024)])
+def test_add_rmsnorm_partials(M, N, K):
+    """Partials + residual + RMSNorm in one kernel == RESID epilogue then q3_rmsnorm, bit for bit."""
+    x, w = rnd((M, K), 1.0, 21), rnd((N, K), 0.02, 22)
+    res = rnd((M, N), 1.0, 23)
+    gain = (1 + rnd((N,), 0.2, 24).float()).to(torch.bfloat16)
+    wt = torch.empty(N, K, dtype=torch.bfloat16, device=DEV)
+    call("q3_tile16", P(dv(w)), N, K, P(wt), S())
+    splits = call("q3_skinny_splits", M, N, K)
+    ws = torch.empty(splits * M * N, dtype=torch.float32, device=DEV)
+    xd, gd = dv(x), dv(gain)
+    r1, r2 = dv(res), dv(res)
+    y1 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    y2 = torch.empty_like(y1)
+    call("q3_skinny_tiled", P(xd), K, P(wt), M, N, K, _lib.EPI_RESID, P(r1), N, P(ws), S())
+    call("q3_rmsnorm", P(r1), N, P(gd), P(y1), N, M, N, 1e-6, S())
+    call("q3_skinny_partials", P(xd), K, P(wt), M, N, K, P(ws), S())
+    call("q3_add_rmsnorm_partials", P(ws), splits, P(r2), P(gd), P(y2), M, N, 1e-6, S())
+    torch.cuda.synchronize()
+    assert torch.equal(r1.cpu(), r2.cpu()) and torch.equal(y1.cpu(), y2.cpu())
+    assert not torch.equal(r2.cpu(), res)
+
+
+@pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6)])
+def test_attn_decode_qkv_partials(B, C, pos, qsplits):
+    """q/k/v from FP32 split partials == from their in-order sum rounded to BF16, bit for bit."""
+    Hq, Hkv, D = 32, 8, 128
+    width = (Hq + 2 * Hkv) * D
+    part = (torch.randn(qsplits, B, width, generator=torch.Generator().manual_seed(pos)) * 0.7).float()
+    acc = part[0].clone()
+    for sp in range(1, qsplits):
+        acc += part[sp]
+    qkv = acc.to(torch.bfloat16)
+    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    splits = call("q3_attn_splits", B, Hkv, C)
+    outs, caches = [], []
+    for use_part in (False, True):
+        ckd, cvd = dv(ck), dv(cv)
+        pacc = torch.empty(B, Hq, splits, D, dtype=torch.float32, device=DEV)
+        pml = torch.empty(B, Hq, splits, 2, dtype=torch.float32, device=DEV)
+        out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+        src = (None, width, P(dv(part)), qsplits) if use_part else (P(dv(qkv)), width, None, 0)
+        call("q3_attn_decode", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)),
+             P(dv(torch.tensor([pos]))), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6,
+             D ** -0.5, S())
+        call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+        caches.append((ckd.cpu(), cvd.cpu()))
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
