@@ -50,7 +50,7 @@ const char *q3_error_string(int code);
  * fused.py:115 add_norm) and the residual / SwiGLU / argmax that follow it.
  * W is [N, K]; K % 8 == 0; x, W 16-byte aligned; ldx % 8 == 0.  Modes:
  * X_EMBED_NORM with EPI_STORE; X_PLAIN with EPI_STORE or EPI_RESID; X_NORM
- * with any epilogue.  EPI_SWIGLU writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
+ * with any epilogue.  EPI_SWIGLU (N % 4 == 0) writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
  * [q3_gemv_partials(M, N, epi), M]; with tokens != NULL the last workgroup
  * also reduces them into tokens[M] (int64), advances *pos when pos != NULL,
  * and resets *counter (a device int, zero before the first call); otherwise
@@ -145,13 +145,16 @@ int q3_qk_norm_rope_kv(const uint16_t *qkv, int ld_qkv, const uint16_t *q_norm_w
  * cache_k/v [B, Hkv, capacity, 128].
  * Writes per-split partials part_acc [B, Hq, splits, 128] (FP32, unnormalised)
  * and part_ml [B, Hq, splits, 2] (running max, sum); q3_attn_merge finishes.
- * Any splits >= 1 is valid; q3_attn_splits gives the tuned count.
- * decode_attention_gqa / _split (fused.py:641-846). */
+ * With splits == 1 and out != NULL the normalised output out [B, Hq*128]
+ * (BF16, what q3_attn_merge would write) is written directly and the partial
+ * buffers are unused.  Any splits >= 1 is valid; q3_attn_splits gives the
+ * tuned count.  decode_attention_gqa / _split (fused.py:641-846). */
 int q3_attn_decode(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
                    const uint16_t *q_norm_w,
                    const uint16_t *k_norm_w, const uint16_t *cos_table,
                    const uint16_t *sin_table, const int64_t *pos,
                    uint16_t *cache_k, uint16_t *cache_v, float *part_acc, float *part_ml,
+                   uint16_t *out,
                    int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                    hipStream_t stream);
 /* Log-sum-exp merge of the splits: out [B, Hq*128] BF16 (fused.py:793-823). */

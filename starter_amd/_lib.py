@@ -42,7 +42,7 @@ SIGNATURES = {
     "q3_add_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "q3_embed_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "q3_qk_norm_rope_kv": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
-    "q3_attn_decode": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P],
+    "q3_attn_decode": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P],
     "q3_attn_merge": [_P, _P, _P, _I, _I, _I, _P],
     "q3_attn_splits": [_I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],

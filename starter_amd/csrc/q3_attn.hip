@@ -141,6 +141,7 @@ struct DecodeArgs {
     bf16_t* cache_v;
     float* part_acc;
     float* part_ml;
+    bf16_t* out;  // with one split: the normalised output [B, Hq*D] directly (no merge)
     int Hq, Hkv, capacity, splits;
     float eps, scale;
 };
@@ -262,7 +263,8 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // split's key range with two register sets in flight (the loop is unrolled by
 // two so neither set is ever copied: a copy would wait for the newest loads,
 // as vector memory counters retire in order); the four waves merge through
-// LDS; attn_merge_kernel merges the splits.
+// LDS; attn_merge_kernel merges the splits, or with one split the normalised
+// output is written here.
 __global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -395,6 +397,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(DecodeArgs a) {
             }
         }
         const int qh = kvh * GROUP + h;
+        if (a.out != nullptr) {  // one split: what attn_merge_kernel would write
+            a.out[((int64_t)b * a.Hq + qh) * D + d] = (bf16_t)f2bf(sl > 0.f ? sacc / sl : 0.f);
+            continue;
+        }
         const int64_t p = ((int64_t)b * a.Hq + qh) * a.splits + split;
         a.part_acc[p * D + d] = sacc;
         if (d == 0) {
@@ -569,14 +575,18 @@ __global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, 
 }  // namespace
 
 extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
-    // About 1024 workgroups (two resident per CU, two rounds) with at least
-    // 256 keys (two blocks per wave) per split; when even that leaves CUs idle
-    // (short contexts at small batch), 128 keys per split to spread the
-    // latency-bound work.
+    // One split (no merge launch: the kernel writes the output) once there are
+    // enough (sequence, KV head) pairs to occupy half the CUs at moderate
+    // context, or every CU twice at any context.  Otherwise about 1024
+    // workgroups (two resident per CU, two rounds) with at least 256 keys (two
+    // blocks per wave) per split; when even that leaves CUs idle (short
+    // contexts at small batch), 128 keys per split to spread the latency-bound
+    // work.
     const long heads = (long)B * Hkv;
+    if (heads >= 512 || (heads >= 128 && capacity <= 4096)) return 1;
     const long want = (1024 + heads - 1) / heads;
     long most = (capacity + 255) / 256;
-    if (heads * most < 256) most = (capacity + 127) / 128;
+    if (heads * most < 128) most = (capacity + 127) / 128;
     const long s = want < most ? want : most;
     return s < 1 ? 1 : (int)s;
 }
@@ -585,16 +595,16 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
                               const bf16_t* q_norm_w,
                               const bf16_t* k_norm_w, const bf16_t* cos_table,
                               const bf16_t* sin_table, const int64_t* pos,
-                              bf16_t* cache_k, bf16_t* cache_v, float* part_acc, float* part_ml,
+                              bf16_t* cache_k, bf16_t* cache_v, float* part_acc, float* part_ml, bf16_t* out,
                               int B, int Hq, int Hkv, int capacity, int splits, float eps, float scale,
                               hipStream_t stream) {
     if (B < 1 || Hkv < 1 || Hq != GROUP * Hkv || capacity < 1 || splits < 1 || ld_qkv < (Hq + 2 * Hkv) * D)
         return (int)hipErrorInvalidValue;
     if ((!qkv && !qkv_part) || (qkv_part && (qkv_splits < 1 || (reinterpret_cast<uintptr_t>(qkv_part) & 3))) ||
-        !pos || !cache_k || !cache_v || !part_acc || !part_ml)
+        !pos || !cache_k || !cache_v || (out ? splits != 1 : (!part_acc || !part_ml)))
         return (int)hipErrorInvalidValue;
     DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
-                 part_acc, part_ml, Hq, Hkv, capacity, splits, eps, scale};
+                 part_acc, part_ml, out, Hq, Hkv, capacity, splits, eps, scale};
     hipLaunchKernelGGL(attn_decode_kernel, dim3(splits, Hkv, B), dim3(THREADS), 0, stream, a);
     Q3_CHECK_LAUNCH();
 }

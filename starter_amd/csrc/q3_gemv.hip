@@ -73,26 +73,45 @@ __device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
         __syncthreads();
         return;
     } else {
+        // One round trip: the rows and the gain are loaded together and kept in
+        // registers (K <= 4096: at most two chunks per thread), squared and
+        // summed, block-reduced, then normalised straight into LDS.
+        constexpr int NC = Q3_GEMV_MAX_NORM_K / 8 / GEMV_THREADS;
         __shared__ float red[GEMV_WAVES][M];
+        uint4 xv[NC][M], gv[NC];
         float ss[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) ss[m] = 0.f;
-        for (int c = tid; c < chunks; c += GEMV_THREADS) {
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const bf16_t* src;
-                if (XMODE == Q3_X_EMBED_NORM) src = a.x + a.ids[m] * (int64_t)a.K;
-                else src = a.x + (int64_t)m * a.ldx;
-                uint4 v = *reinterpret_cast<const uint4*>(src + c * 8);
-                *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) = v;
-                if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
-                    *reinterpret_cast<uint4*>(a.resid_out + (int64_t)m * a.K + c * 8) = v;
-                float s = ss[m];
-                s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
-                s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
-                s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
-                s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
-                ss[m] = s;
+        for (int j = 0; j < NC; ++j) {
+            const int c = tid + j * GEMV_THREADS;
+            if (c < chunks) {
+                gv[j] = *reinterpret_cast<const uint4*>(a.norm_w + c * 8);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const bf16_t* src;
+                    if (XMODE == Q3_X_EMBED_NORM) src = a.x + a.ids[m] * (int64_t)a.K;
+                    else src = a.x + (int64_t)m * a.ldx;
+                    xv[j][m] = *reinterpret_cast<const uint4*>(src + c * 8);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = tid + j * GEMV_THREADS;
+            if (c < chunks) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint4 v = xv[j][m];
+                    if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
+                        *reinterpret_cast<uint4*>(a.resid_out + (int64_t)m * a.K + c * 8) = v;
+                    float s = ss[m];
+                    s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
+                    s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
+                    s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
+                    s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
+                    ss[m] = s;
+                }
             }
         }
 #pragma unroll
@@ -107,18 +126,21 @@ __device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
             float s = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
             inv[m] = inv_rms(s, a.K, a.eps);
         }
-        for (int c = tid; c < chunks; c += GEMV_THREADS) {
-            uint4 g = *reinterpret_cast<const uint4*>(a.norm_w + c * 8);
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                uint4* p = reinterpret_cast<uint4*>(xs + m * a.K + c * 8);
-                uint4 v = *p;
-                float im = inv[m];
-                v.x = pack2(norm_elem(bflo(v.x), im, bflo(g.x)), norm_elem(bfhi(v.x), im, bfhi(g.x)));
-                v.y = pack2(norm_elem(bflo(v.y), im, bflo(g.y)), norm_elem(bfhi(v.y), im, bfhi(g.y)));
-                v.z = pack2(norm_elem(bflo(v.z), im, bflo(g.z)), norm_elem(bfhi(v.z), im, bfhi(g.z)));
-                v.w = pack2(norm_elem(bflo(v.w), im, bflo(g.w)), norm_elem(bfhi(v.w), im, bfhi(g.w)));
-                *p = v;
+        for (int j = 0; j < NC; ++j) {
+            const int c = tid + j * GEMV_THREADS;
+            if (c < chunks) {
+                const uint4 g = gv[j];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    uint4 v = xv[j][m];
+                    const float im = inv[m];
+                    v.x = pack2(norm_elem(bflo(v.x), im, bflo(g.x)), norm_elem(bfhi(v.x), im, bfhi(g.x)));
+                    v.y = pack2(norm_elem(bflo(v.y), im, bflo(g.y)), norm_elem(bfhi(v.y), im, bfhi(g.y)));
+                    v.z = pack2(norm_elem(bflo(v.z), im, bflo(g.z)), norm_elem(bfhi(v.z), im, bfhi(g.z)));
+                    v.w = pack2(norm_elem(bflo(v.w), im, bflo(g.w)), norm_elem(bfhi(v.w), im, bfhi(g.w)));
+                    *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) = v;
+                }
             }
         }
         __syncthreads();
@@ -307,11 +329,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
 }
 
 // Rows per wave.  Projections: one row per wave, so the N rows spread over N
-// waves and every CU streams.  SwiGLU needs the (gate, up) pair.  The LM-head
+// waves and every CU streams.  SwiGLU takes two (gate, up) pairs: gate_up's
+// 19456 rows then make 1216 workgroups, all resident at once (two rows per
+// wave leave a second, mostly idle round).  The LM-head
 // argmax (N ~ 152k) has waves to spare and takes four rows (two at M > 4),
 // which keeps its partials few.
 constexpr int rows_per_wave(int M, int epi) {
-    return epi == Q3_EPI_SWIGLU ? 2
+    return epi == Q3_EPI_SWIGLU ? 4
          : (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) ? (M > 4 ? 2 : 4)
          : 1;
 }

@@ -347,8 +347,9 @@ class Engine:
             call("q3_attn_decode", qkv, self.qkv_size, None, 0, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
                  vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
-                 B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
-            call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+                 attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
+            if self.splits > 1:
+                call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
             if self.small:
                 call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
                      B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
@@ -397,8 +398,9 @@ class Engine:
             call("q3_attn_decode", None, self.qkv_size, ws, s_qkv, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                  _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
                  vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
-                 B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
-            call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+                 attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
+            if self.splits > 1:
+                call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
             call("q3_skinny_partials", attn, self.q_size, T(L["o"]), B, H, self.q_size, ws, s)
             call("q3_add_rmsnorm_partials", ws, s_o, resid, _ptr(L["post_ln"]), nbuf, B, H, self.EPS, s)
             call("q3_skinny_tiled", nbuf, H, T(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, ws, s)

@@ -305,7 +305,8 @@ def attention_oracle(q, ck, cv, length, scale):
 @pytest.mark.parametrize("B,C,pos,splits", [(1, 64, 0, 1), (1, 64, 31, 1), (2, 64, 32, 1), (1, 300, 200, 3),
                                             (3, 300, 299, 5), (2, 1536, 1100, 12), (1, 1536, 1535, 12),
                                             (2, 700, 255, 40), (1, 700, 699, 1), (2, 1000, 900, 2),
-                                            (1, 2176, 2100, 2), (1, 3000, 2999, 3)])
+                                            (1, 2176, 2100, 2), (1, 3000, 2999, 3), (1, 1536, 1300, 1),
+                                            (4, 2048, 2047, 1), (40, 300, 290, 1)])
 def test_attn_decode(B, C, pos, splits):
     Hq, Hkv, D = 32, 8, 128
     width = (Hq + 2 * Hkv) * D
@@ -322,15 +323,21 @@ def test_attn_decode(B, C, pos, splits):
     posd = torch.tensor([pos], dtype=torch.int64, device=DEV)
     qkvd, qwd, kwd, cosd, sind = dv(qkv), dv(qw), dv(kw), dv(cos), dv(sin)
     call("q3_attn_decode", P(qkvd), width, None, 0, P(qwd), P(kwd), P(cosd), P(sind),
-         P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
+         P(posd), P(ckd), P(cvd), P(pacc), P(pml), None, B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
     # A second call (the row at pos now already holds the new key): same bits.
     again = torch.empty_like(out)
     call("q3_attn_decode", P(qkvd), width, None, 0, P(qwd), P(kwd), P(cosd), P(sind),
-         P(posd), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
+         P(posd), P(ckd), P(cvd), P(pacc), P(pml), None, B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
     call("q3_attn_merge", P(pacc), P(pml), P(again), B, Hq, splits, S())
     torch.cuda.synchronize()
     assert torch.equal(again.cpu(), out.cpu())
+    if splits == 1:  # direct output: what the merge kernel writes for one split
+        direct = torch.empty_like(out)
+        call("q3_attn_decode", P(qkvd), width, None, 0, P(qwd), P(kwd), P(cosd), P(sind), P(posd), P(ckd),
+             P(cvd), None, None, P(direct), B, Hq, Hkv, C, 1, 1e-6, D ** -0.5, S())
+        torch.cuda.synchronize()
+        assert torch.equal(direct.cpu(), out.cpu())
     x = qkv.view(B, 1, Hq + 2 * Hkv, D)
     c, s_ = cos[pos].view(1, 1, 1, D), sin[pos].view(1, 1, 1, D)
     q = oc.apply_rope(oc.rms_norm(x[:, :, :Hq], qw, 1e-6), c, s_)[:, 0]
@@ -518,7 +525,7 @@ def test_attn_decode_qkv_partials(B, C, pos, qsplits):
         out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
         src = (None, width, P(dv(part)), qsplits) if use_part else (P(dv(qkv)), width, None, 0)
         call("q3_attn_decode", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)),
-             P(dv(torch.tensor([pos]))), P(ckd), P(cvd), P(pacc), P(pml), B, Hq, Hkv, C, splits, 1e-6,
+             P(dv(torch.tensor([pos]))), P(ckd), P(cvd), P(pacc), P(pml), None, B, Hq, Hkv, C, splits, 1e-6,
              D ** -0.5, S())
         call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
         torch.cuda.synchronize()
