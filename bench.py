@@ -41,7 +41,7 @@ def weight_bytes(eng) -> int:
     return total
 
 
-def dominant_kernel_roofline(eng, reps: int = 20) -> dict:
+def dominant_kernel_roofline(eng, config: int, reps: int = 20) -> dict:
     """Average duration of the gate/up GEMV (norm prologue + SwiGLU epilogue)
     over all 36 layers' weights, captured as one graph and replayed.
 
@@ -79,8 +79,22 @@ def dominant_kernel_roofline(eng, reps: int = 20) -> dict:
     achieved = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "kernel": "gemv_dot2 gate_up (norm prologue, SwiGLU epilogue)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(f"gemv_gate_up_config{config}_b{B}_traffic.txt"),
             "bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3, 2)}
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary
+    (``profiles/<name>``, counters scaled by a plain copy of known size), or None
+    when no such measurement exists for this kernel and workload."""
+    path = pathlib.Path(__file__).resolve().parent / "profiles" / name
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
 
 
 def cpu_baseline(wl, ckpt, budget_s: float = 20.0) -> dict:
@@ -115,6 +129,23 @@ def cpu_baseline(wl, ckpt, budget_s: float = 20.0) -> dict:
                       f"on a pre-filled cache; CPU oracle (PyTorch BF16, oracle/qwen3_cpu.py)"}
 
 
+def copy_probe(nbytes: int = 1 << 30) -> int:
+    """A plain copy of ``nbytes`` (reads nbytes, writes nbytes), three times.
+
+    Under ``rocprofv3 --pmc FETCH_SIZE`` (or WRITE_SIZE) its per-dispatch
+    reading against the known 1 GiB gives the counter's scale on this device.
+    """
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: 3 copies of {nbytes} bytes")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,11 +154,16 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--ckpt-dir", default=os.environ.get("Q3_CKPT_DIR", "/tmp/q3_seeded_qwen3_4b"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (3 times): the known-size "
+                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(one MI355X per box); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe()
 
     sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent))
     import torch
@@ -175,7 +211,7 @@ def main() -> int:
     ctx_mean = P + W + (K + 1) / 2
     step_bytes = wbytes + B * ctx_mean * KV_BYTES_PER_TOKEN + B * KV_BYTES_PER_TOKEN
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    roof = dominant_kernel_roofline(eng)
+    roof = dominant_kernel_roofline(eng, args.config)
     log(f"{ms_step:.3f} ms/step, {value:.1f} tok/s, step HBM {step_gbs:.0f} GB/s "
         f"({step_gbs / HBM_PEAK_GBS:.1%}); gate_up GEMV {roof.get('achieved')} GB/s")
 
