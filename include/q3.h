@@ -180,6 +180,49 @@ int q3_argmax_finish(const float *part_val, const int *part_idx, int nparts, int
 int q3_argmax_rows(const uint16_t *logits, int ld, int B, int V, int64_t *tokens,
                    int64_t *pos, hipStream_t stream);
 
+/* ---- whole-step persistent decode, one sequence ------------------------------ */
+
+/* One layer's device pointers (BF16 [N, K] row-major weights and gains), as the
+ * persistent kernel reads them from a device array of L entries. */
+typedef struct q3_layer {
+    const uint16_t *qkv;     /* [(Hq + 2 Hkv) * 128, H]: q | k | v rows          */
+    const uint16_t *o;       /* [H, Hq * 128]                                     */
+    const uint16_t *gate_up; /* [2 I, H], rows (gate_j, up_j) interleaved         */
+    const uint16_t *down;    /* [H, I]                                            */
+    const uint16_t *in_ln, *post_ln, *q_norm, *k_norm; /* [H], [H], [128], [128]  */
+} q3_layer;
+
+/* The whole self-feeding decode step of one sequence (B = 1) in one launch of
+ * `grid` workgroups (q3_persist_grid(): one per CU, all resident): embedding,
+ * L x (RMSNorm, qkv, q/k RMSNorm + RoPE + KV append, split attention + merge,
+ * o + residual, RMSNorm, gate/up + SwiGLU, down + residual), final RMSNorm, LM
+ * head, greedy argmax into tokens[0], *pos += 1.  Replaces the captured
+ * _forward_decode step (engine.py:805-839) as one kernel instead of one per op.
+ * cache_k/v [L, 1, Hkv, capacity, 128]; cos/sin [>= capacity, 128]; logits
+ * [V] BF16 stored when non-NULL.  work: q3_persist_work_bytes() bytes, 256-byte
+ * aligned, zeroed once before the first call and then owned by this entry point
+ * (it carries a step epoch between calls; re-zero it after an error).  Shapes:
+ * H, I, Hq*128 multiples of 512, H <= 4096, I <= 16384, Hq == 4 Hkv, and
+ * q3_persist_supported() true.  A launch that cannot complete (a workgroup not
+ * resident, a wait past 1 s) writes tokens[0] = -1 and exits.  trace: NULL,
+ * or q3_persist_trace_words(L) words of timestamps (below). */
+int q3_persist_grid(void);
+int q3_persist_supported(int L, int H, int I, int V, int Hq, int Hkv, int capacity, int grid);
+int64_t q3_persist_work_bytes(int H, int I, int Hq, int Hkv, int grid);
+int q3_decode_persistent(const q3_layer *layers, int L, const uint16_t *embed, const uint16_t *final_norm,
+                         const uint16_t *lm_head, int H, int I, int V, int Hq, int Hkv,
+                         const uint16_t *cos_t, const uint16_t *sin_t, uint16_t *cache_k, uint16_t *cache_v,
+                         int capacity, int64_t *tokens, int64_t *pos, void *work, int grid, uint16_t *logits,
+                         float eps, float scale, uint64_t *trace, hipStream_t stream);
+/* Words of the optional step trace of q3_decode_persistent (trace != NULL):
+ * for workgroups 0, 1, grid/2 and grid-1, per layer 16 wall-clock (100 MHz)
+ * stamps of the control wave's phase boundaries, then two stamps per streamed
+ * matrix from streamer wave 0 (began waiting for the input, saw it); then, for
+ * every workgroup and layer, [L][grid][4] stamps (qkv done, attention inputs
+ * ready, attention done, merge done).  A diagnostic: steps run slower while
+ * tracing. */
+int q3_persist_trace_words(int L, int grid);
+
 /* hipGraph capture of everything enqueued on `stream` between begin and end
  * (engine.py:1029-1065). */
 int q3_graph_begin(hipStream_t stream);

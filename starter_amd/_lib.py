@@ -48,15 +48,22 @@ SIGNATURES = {
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P],
     "q3_argmax_rows": [_P, _I, _I, _I, _P, _P, _P],
+    "q3_persist_grid": [],
+    "q3_persist_supported": [_I, _I, _I, _I, _I, _I, _I, _I],
+    "q3_persist_work_bytes": [_I, _I, _I, _I, _I],
+    "q3_decode_persistent": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P,
+                             _F, _F, _P, _P],
+    "q3_persist_trace_words": [_I, _I],
     "q3_graph_begin": [_P],
     "q3_graph_end": [_P, ctypes.POINTER(ctypes.c_void_p)],
     "q3_graph_launch": [_P, _P],
     "q3_graph_destroy": [_P],
 }
-_RESTYPES = {"q3_error_string": ctypes.c_char_p}
+_RESTYPES = {"q3_error_string": ctypes.c_char_p, "q3_persist_work_bytes": ctypes.c_int64}
 
 #: entry points that return a count, not an error code
-_COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_skinny_splits", "q3_skinny_ws_floats"}
+_COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_skinny_splits", "q3_skinny_ws_floats",
+           "q3_persist_grid", "q3_persist_supported", "q3_persist_work_bytes", "q3_persist_trace_words"}
 
 _LIB: ctypes.CDLL | None = None
 

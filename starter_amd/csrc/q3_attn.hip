@@ -17,21 +17,18 @@
 // is mapped to key kappa(g,t) = t<4 ? 4g+t : 16+4g+t-4, and V^T is read from
 // an LDS tile with the same key order.  The order of a reduction is free; the
 // pairing of operands is what matters.
+#include "q3_attn_mfma.hpp"
 #include "q3_common.hpp"
 #include "q3.h"
 
 namespace {
 
+using namespace q3attn;
+
 constexpr int D = 128;
 constexpr int GROUP = 4;     // query heads per KV head
 constexpr int BLK = 32;      // keys per block
 constexpr int THREADS = 256; // 4 waves
-
-// Decode K/V tiles in LDS: [32 keys][16 chunks of 16 bytes], chunk c of key r
-// stored at slot c ^ (r & 15).  Rows arrive whole (1 KB = four keys per load
-// instruction); K operand reads (16 keys at one chunk) and the transposed V
-// reads then spread over all banks.
-__device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
 // LDS V tile of the prefill kernel [32 keys][128 d] BF16, 16-byte chunks
 // swizzled so the column reads for keys kappa(g, t) hit four distinct bank groups.
@@ -53,62 +50,6 @@ __device__ __forceinline__ bf16x8_t vt_operand(const bf16_t* vs, int dm, int n, 
     }
     uint4 v = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
     return as_bf16x8(v);
-}
-
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-#define Q3_LDS(p) ((__attribute__((address_space(3))) i16x4_t*)(p))
-
-// The same operand from a decode V tile with two ds_read_b64_tr_b16: within
-// each 16-lane group, lane i names 4 consecutive d of one key (key 4*(i/4) +
-// base, d = 16dm + 4*(i%4)); the transpose hands lane n the element d = 16dm + n
-// of the four keys.  Keys 4g..4g+3 fill k slots 0-3, keys 16+4g.. slots 4-7.
-__device__ __forceinline__ bf16x8_t vt_operand_tr(const bf16_t* vt, int dm, int lane) {
-    const int g = lane >> 4, i = lane & 15;
-    const int c = 2 * dm + ((i & 3) >> 1), half = (i & 1) * 4;
-    const int r0 = 4 * g + (i >> 2), r1 = r0 + 16;
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r0, c) * 8 + half));
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r1, c) * 8 + half));
-    typedef short i16x8_t __attribute__((ext_vector_type(8)));
-    const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8_t, v);
-}
-
-// B operand (P^T) from the two score blocks held by this lane.
-__device__ __forceinline__ bf16x8_t p_operand(const float p0[4], const float p1[4]) {
-    uint4 v = make_uint4(pack2(f2bf(p0[0]), f2bf(p0[1])), pack2(f2bf(p0[2]), f2bf(p0[3])),
-                         pack2(f2bf(p1[0]), f2bf(p1[1])), pack2(f2bf(p1[2]), f2bf(p1[3])));
-    return as_bf16x8(v);
-}
-
-// Max / sum over the four lane groups that hold one query's keys.
-__device__ __forceinline__ float group_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, Q3_WAVE));
-    return fmaxf(v, __shfl_xor(v, 32, Q3_WAVE));
-}
-__device__ __forceinline__ float group_sum(float v) {
-    v += __shfl_xor(v, 16, Q3_WAVE);
-    return v + __shfl_xor(v, 32, Q3_WAVE);
-}
-
-// Online-softmax update of one 32-key block for this lane's query.
-// s0/s1 hold scaled scores (masked = -inf); returns alpha, updates m/l and
-// turns s0/s1 into probabilities.
-__device__ __forceinline__ float softmax_block(float s0[4], float s1[4], float& m, float& l) {
-    float bm = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                     fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-    bm = group_max(bm);
-    const float m_new = fmaxf(m, bm);
-    const float alpha = expf(m - m_new);
-    float ps = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        s0[i] = expf(s0[i] - m_new);
-        s1[i] = expf(s1[i] - m_new);
-        ps += s0[i] + s1[i];
-    }
-    l = l * alpha + group_sum(ps);
-    m = m_new;
-    return alpha;
 }
 
 // Per-head RMSNorm + RoPE of one 128-wide row held as (lo = x[l], hi = x[l+64])
@@ -209,54 +150,16 @@ __device__ __forceinline__ int split_len(int capacity, int splits) {
     return (per + BLK - 1) / BLK * BLK;
 }
 
-struct WaveState {
-    bf16x8_t qb[4];
-    f32x4_t acc[8];
-    float m, l;
-};
-
-// One 32-key block: registers -> this wave's LDS tiles (the new token's row
-// substituted), S^T = K.Q^T, online softmax, O^T += V^T.P^T.
+// One 32-key block: registers -> this wave's LDS tiles, then the block.
 __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf16_t* kt, bf16_t* vt, int blk,
                                              int end, int sub_row, const bf16_t* knew, const bf16_t* vnew,
                                              float scale, int lane) {
-    const int g = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         reinterpret_cast<u32x4_t*>(kt)[64 * j + lane] = r.k[j];
         reinterpret_cast<u32x4_t*>(vt)[64 * j + lane] = r.v[j];
     }
-    if (sub_row >= 0) {  // the appended token replaces whatever the cache held at pos
-        if (lane < 16) {
-            reinterpret_cast<u32x4_t*>(kt)[kv_slot(sub_row, lane)] = reinterpret_cast<const u32x4_t*>(knew)[lane];
-            reinterpret_cast<u32x4_t*>(vt)[kv_slot(sub_row, lane)] = reinterpret_cast<const u32x4_t*>(vnew)[lane];
-        }
-    }
-    f32x4_t s[2];
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-        s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const int key = 16 * hb + n;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const u32x4_t kv = reinterpret_cast<const u32x4_t*>(kt)[kv_slot(key, 4 * kk + g)];
-            s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), st.qb[kk], s[hb], 0,
-                                                            0, 0);
-        }
-    }
-    float s0[4], s1[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        s0[i] = (blk + 4 * g + i < end) ? s[0][i] * scale : -INFINITY;
-        s1[i] = (blk + 16 + 4 * g + i < end) ? s[1][i] * scale : -INFINITY;
-    }
-    const float alpha = softmax_block(s0, s1, st.m, st.l);
-    const bf16x8_t pb = p_operand(s0, s1);
-#pragma unroll
-    for (int dm = 0; dm < 8; ++dm) {
-        st.acc[dm] *= alpha;
-        st.acc[dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand_tr(vt, dm, lane), pb, st.acc[dm], 0, 0, 0);
-    }
+    decode_block_tiles(st, kt, vt, blk, end, sub_row, knew, vnew, scale, lane);
 }
 
 // grid (splits, Hkv, B); wave w of a workgroup takes blocks w, w+4, ... of the

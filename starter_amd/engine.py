@@ -43,6 +43,7 @@ that do not tile, the LDS-tiled MFMA GEMM with separate norm kernels.
 from __future__ import annotations
 
 import ctypes
+import os
 import sys
 import time
 
@@ -70,6 +71,13 @@ MEMORY_MARGIN_BYTES = 2 << 30
 #: the GEMV's VALU-bound dot products; above that the LDS-tiled GEMM.
 GEMV_BATCH_MAX = 4
 SKINNY_BATCH_MAX = 64
+
+#: One sequence decodes in a single persistent kernel per step
+#: (``q3_decode_persistent``) when the shapes allow it; False keeps the
+#: kernel-per-op step (tests compare the two).  Off by default until the
+#: one-kernel step is the faster of the two (2.49 vs 2.01 ms per step at
+#: config 2 so far).  Environment override: Q3_PERSISTENT_DECODE=0 / 1.
+PERSISTENT_DECODE = os.environ.get("Q3_PERSISTENT_DECODE", "0") != "0"
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -176,6 +184,11 @@ class Engine:
         self._grow_rope(4096)
 
         self.tiled = None  # 16-row tiled weight copies, made on first use
+        self.persist = False
+        #: Optional device buffer (int64, q3_persist_trace_words(L)) that the
+        #: one-kernel step fills with phase timestamps; set before the graph is
+        #: captured (a diagnostic, see q3.h).
+        self.persist_trace: torch.Tensor | None = None
         self.batch = 0
         self.capacity = 0
         self.cache_k = self.cache_v = None
@@ -248,6 +261,7 @@ class Engine:
         self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
         self.small = B <= GEMV_BATCH_MAX
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
+        self.persist = B == 1 and PERSISTENT_DECODE and self._persist_setup(capacity)
         # Split-K workspace of the MFMA decode projections: every projection's
         # partials, [splits, B, N] FP32, one consumer at a time.
         ws = 0
@@ -265,6 +279,25 @@ class Engine:
             self.part_idx = self._empty(self.lm_parts, B, dtype=torch.int32)
         self.logits = self._empty(B, V)
         self._capture()
+
+    def _persist_setup(self, capacity: int) -> bool:
+        """Buffers of the one-kernel decode step (B = 1): the device table of layer
+        pointers and the zeroed exchange/work buffer.  False when the device or the
+        model shape does not admit it (then the kernel-per-op step runs)."""
+        grid = call("q3_persist_grid")
+        if grid < 1:
+            return False
+        grid -= grid % self.KV_HEADS
+        if not call("q3_persist_supported", self.LAYERS, self.HIDDEN, self.INTER, self.VOCAB, self.HEADS,
+                    self.KV_HEADS, capacity, grid):
+            return False
+        table = [[L[k].data_ptr() for k in ("qkv", "o", "gate_up", "down", "in_ln", "post_ln", "q_norm", "k_norm")]
+                 for L in self.layers]
+        self.persist_layers = torch.tensor(table, dtype=torch.int64, device=self.device)
+        nbytes = call("q3_persist_work_bytes", self.HIDDEN, self.INTER, self.HEADS, self.KV_HEADS, grid)
+        self.persist_work = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        self.persist_grid = grid
+        return True
 
     def _projections(self) -> list[tuple[int, int]]:
         """(N, K) of qkv, o, gate_up, down and the LM head."""
@@ -316,6 +349,14 @@ class Engine:
 
     def _enqueue_decode(self) -> None:
         """One self-feeding decode step on ``self.stream`` (reference ``_forward_decode``)."""
+        if self.persist:
+            call("q3_decode_persistent", _ptr(self.persist_layers), self.LAYERS, _ptr(self.embed),
+                 _ptr(self.final_norm), _ptr(self.lm_head), self.HIDDEN, self.INTER, self.VOCAB, self.HEADS,
+                 self.KV_HEADS, _ptr(self.cos_table), _ptr(self.sin_table), _ptr(self.cache_k),
+                 _ptr(self.cache_v), self.capacity, _ptr(self.g_token), _ptr(self.g_pos), _ptr(self.persist_work),
+                 self.persist_grid, _ptr(self.logits) if self.keep_logits else None, self.EPS, self.SCALE,
+                 _ptr(self.persist_trace), self._s)
+            return
         if self.skinny:
             self._enqueue_decode_skinny()
             return
@@ -425,10 +466,12 @@ class Engine:
         with torch.cuda.stream(self.stream):
             for _ in range(2):
                 self.g_pos.fill_(max(0, self.capacity - 2))
+                self.g_token.zero_()
                 self._enqueue_decode()
             self.g_pos.zero_()
             self.g_token.zero_()
         self.stream.synchronize()
+        self._check_step()
         call("q3_graph_begin", self._s)
         try:
             self._enqueue_decode()
@@ -447,6 +490,20 @@ class Engine:
         """Replay the captured step: g_token <- next token, g_pos += 1."""
         call("q3_graph_launch", self.graph, self._s)
         return self.g_token
+
+    def _check_step(self, tokens: list[int] | None = None) -> None:
+        """The one-kernel step reports a launch that could not complete (a wait
+        past its time bound) as token -1; raise, and drop the step's state so the
+        next call rebuilds it."""
+        if not self.persist:
+            return
+        if tokens is None:
+            tokens = self.g_token.cpu().tolist()
+        if min(tokens) < 0:
+            code = int(self.persist_work[4:8].view(torch.int32).cpu()[0])
+            self.graph_key_reset()
+            raise RuntimeError(f"q3_decode_persistent did not complete (error {code}): a workgroup "
+                               "waited past its time bound")
 
     # -------------------------------------------------------------- prefill
 
@@ -565,6 +622,9 @@ class Engine:
             else:
                 done.synchronize()
                 out = host.clone()
+            toks = out.tolist()
+            if self.persist:
+                self._check_step(toks)
             if step + 1 < max_new_tokens:
                 self._decode_step()
                 with torch.cuda.stream(self.stream):
@@ -573,7 +633,7 @@ class Engine:
                 pending = True
             else:
                 pending = False
-            yield out.tolist()
+            yield toks
 
     # -------------------------------------------------------- diagnostics
 
@@ -607,6 +667,7 @@ class Engine:
             self._decode_step()
             self.stream.synchronize()
             steps.append(self.g_token.cpu().tolist())
+            self._check_step(steps[-1])
             kept.append(self.logits.cpu())
         self.keep_logits = False
         self.graph_key_reset()
