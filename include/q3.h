@@ -217,10 +217,12 @@ int q3_decode_persistent(const q3_layer *layers, int L, const uint16_t *embed, c
 /* Words of the optional step trace of q3_decode_persistent (trace != NULL):
  * for workgroups 0, 1, grid/2 and grid-1, per layer 16 wall-clock (100 MHz)
  * stamps of the control wave's phase boundaries, then two stamps per streamed
- * matrix from streamer wave 0 (began waiting for the input, saw it); then, for
- * every workgroup and layer, [L][grid][4] stamps (qkv done, attention inputs
- * ready, attention done, merge done).  A diagnostic: steps run slower while
- * tracing. */
+ * matrix from compute wave 0 (began waiting for the input, saw it), then one
+ * per streamed matrix from loader wave 0 (issued its first unit); then, for
+ * every workgroup and layer, [L][grid][8] words (qkv done, attention inputs
+ * ready, attention done, merge done, merge poll start, merge polls, loader 0's
+ * polls of a full ring, compute wave 0's polls for landed units).  A
+ * diagnostic: steps run slower while tracing. */
 int q3_persist_trace_words(int L, int grid);
 
 /* hipGraph capture of everything enqueued on `stream` between begin and end

@@ -11,18 +11,23 @@
 // cannot start before its input exists.  Here one workgroup per CU lives for the
 // whole step, and the weight stream never waits for an op boundary:
 //
-//  * waves 0..NS-1 ("streamers") walk this workgroup's rows of every weight
+//  * waves 0..NLOAD-1 ("loaders") walk this workgroup's rows of every weight
 //    matrix of the step in order -- qkv, o, gate/up, down of each layer, then
-//    the LM head -- with RING 1 KB loads in flight per wave.  Loads of the next
-//    matrix are issued while the current one's output is still being exchanged
-//    between workgroups.  A row's dot product is summed per lane over its
+//    the LM head -- and copy them, 1 KB unit by unit, straight from HBM into a
+//    96 KB LDS ring (global_load_lds), LDEPTH units in flight per wave.  Units
+//    of the next matrix go out while the current one's output is still being
+//    exchanged between workgroups; a slot is refilled once the unit in it has
+//    been consumed.  The loaders never read what they load, so no wait of
+//    theirs depends on the consumers' pace.
+//  * waves NLOAD..NLOAD+NCOMP-1 ("compute") take rows in turn and read them
+//    from the ring.  A row's dot product is summed per lane over its
 //    512-element chunks in order and then across the wave: the arithmetic and
 //    order of the GEMV kernel (q3_gemv), so every projection matches it bit for
 //    bit.
 //  * the last wave ("control") does everything else: it gathers each matrix's
 //    input vector into LDS (RMSNorm'd where the op has a norm, with the GEMV
-//    prologue's summation order), releases it to the streamers through an LDS
-//    counter, applies the epilogue to the streamers' row sums (residual add,
+//    prologue's summation order), releases it to the compute waves through an
+//    LDS counter, applies the epilogue to their row sums (residual add,
 //    SwiGLU, argmax) and publishes this workgroup's outputs; per layer it also
 //    runs one (KV head, key range) unit of attention -- q/k RMSNorm + RoPE and
 //    the KV append fused in -- and one slice of the split merge.
@@ -53,12 +58,16 @@ constexpr int PGROUP = 4;             // query heads per KV head
 constexpr int CHUNK = 512;            // BF16 elements per streamed unit: 64 lanes x 16 bytes
 constexpr int NWAVES = 8;
 constexpr int PTHREADS = NWAVES * Q3_WAVE;
-constexpr int NS = NWAVES - 1;        // streamer waves; wave NS is the control wave
-#ifndef Q3_PERSIST_RING
-#define Q3_PERSIST_RING 32
+constexpr int NLOAD = 3;              // loader waves 0..2: weights HBM -> LDS ring
+constexpr int NCOMP = 4;              // compute waves 3..6: ring x input -> row sums
+constexpr int CTL_WAVE = NLOAD + NCOMP;  // wave 7: exchange, norms, epilogues, attention
+static_assert(CTL_WAVE == NWAVES - 1, "wave roles");
+constexpr int RU = 96;                // ring units (1 KB each) in LDS
+#ifndef Q3_PERSIST_LDEPTH
+#define Q3_PERSIST_LDEPTH 8
 #endif
-constexpr int RING = Q3_PERSIST_RING;  // streamed units in flight per streamer wave
-constexpr int MAX_X = 16384;          // staged input elements (LDS)
+constexpr int LDEPTH = Q3_PERSIST_LDEPTH;  // ring loads in flight per loader wave
+constexpr int MAX_X = 10240;          // staged input elements (LDS)
 constexpr int MAX_ROWS = 1024;        // row sums per workgroup per matrix
 constexpr int MAX_OWN = 64;           // residual rows owned per workgroup
 constexpr int PREC = 264;             // words per attention partial: acc[128], m, l as (hi, lo) pairs, padded
@@ -66,20 +75,21 @@ constexpr int MAX_SPLITS = 128;       // key ranges per KV head (two per merge l
 constexpr int MAX_SLICE = 16;         // merged outputs per workgroup
 constexpr int STAGE_CHUNKS = 10;      // 8-element chunks per lane gathered per round trip
 constexpr int ATT_KEYS = 64;          // cached keys gathered into LDS per round trip: two 32-key tiles
-constexpr int LDS_BYTES = 96 * 1024;  // more than half of a CU's 160 KB: one workgroup per CU
+constexpr int LDS_BYTES = 160 * 1024; // the whole CU's LDS: one workgroup per CU
 constexpr uint64_t CTL_TIMEOUT = 100000000ull;     // wall-clock ticks (100 MHz): 1 s
 constexpr uint64_t STREAM_TIMEOUT = 200000000ull;  // 2 s: longer than any single control wait
 
 enum { OP_QKV = 0, OP_ATTN, OP_MERGE, OP_O, OP_GU, OP_DOWN, OP_COUNT = 8 };
 
 // Optional step trace (wall clock, 100 MHz): TRACE_WGS workgroups (0, 1, G/2,
-// G-1) record, per layer, TRACE_EV control-wave events and, for streamer wave
-// 0, when it began waiting for each matrix's input and when it saw it.
+// G-1) record, per layer, TRACE_EV control-wave events; per streamed matrix,
+// for compute wave 0, when it began waiting for the input and when it saw it,
+// and for loader 0, when it issued the matrix's first unit.
 constexpr int TRACE_WGS = 4;
 constexpr int TRACE_EV = 16;
 enum {
     T_QKV_IN = 0,   // qkv input gathered (residual ready)
-    T_QKV_DONE,     // streamers finished qkv
+    T_QKV_DONE,     // compute waves finished qkv
     T_ATT_IN,       // q/k/v of this head ready
     T_ATT_DONE,     // partial published
     T_MRG_IN,       // partials ready
@@ -93,10 +103,11 @@ enum {
     T_START = 15,   // layer 0 only: control wave start
 };
 __host__ __device__ constexpr int trace_words(int L) {
-    return TRACE_WGS * ((L + 1) * TRACE_EV + 2 * (4 * L + 1));
+    return TRACE_WGS * ((L + 1) * TRACE_EV + 3 * (4 * L + 1));
 }
-// After those: every workgroup's (qkv done, attention in, attention done, merge
-// done) per layer, [L][G][4], for the skew between workgroups.
+// After those, [L][G][TRACE_ALL] per layer and workgroup: qkv done, attention
+// in, attention done, merge done, merge poll start (wall clock), merge poll
+// count, loader 0's polls of a full ring, compute wave 0's polls for landed units.
 constexpr int TRACE_ALL = 8;
 __host__ __device__ constexpr int trace_words_all(int L, int G) { return trace_words(L) + L * G * TRACE_ALL; }
 __device__ __forceinline__ int trace_slot(int wg, int G) {
@@ -107,6 +118,7 @@ enum { M_QKV = 0, M_O, M_GU, M_DOWN, M_LM };
 enum : uint32_t { ERR_INPUT = 1, ERR_TIMEOUT_X = 2, ERR_TIMEOUT_LDS = 3 };
 
 struct Smem {
+    u32x4_t ring[RU * 64];    // weight units in flight to the compute waves (unit u in slot u % RU)
     bf16_t x[MAX_X];          // the current matrix's input vector
     float rows[MAX_ROWS];     // row sums of the current matrix (this workgroup's rows)
     bf16_t own[MAX_OWN];      // this workgroup's residual rows
@@ -116,11 +128,16 @@ struct Smem {
     bf16_t knew[PD];          //            this token's K (normed, rotated) and V
     bf16_t vnew[PD];
     int pK[5], prb[5], pre[5];  // per streamed-matrix kind: K and this workgroup's rows [rb, re)
-    int ready;                // matrices whose input is staged (control -> streamers)
-    int done;                 // (streamer, matrix) completions (streamers -> control)
+    int poff[5];              // per kind: first unit within a layer (LM: within the LM head)
+    int ulayer;               // units per layer
+    __align__(16) int landed[4];  // per loader wave: its units (every NLOAD-th) landed in the ring
+    __align__(16) int prog[4];    // per compute wave: every unit of its below this index consumed
+    int ready;                // matrices whose input is staged (control -> compute waves)
+    int done;                 // (compute wave, matrix) completions (compute waves -> control)
     int abort;
 };
-static_assert(sizeof(Smem) < LDS_BYTES, "LDS layout");
+static_assert(sizeof(Smem) <= LDS_BYTES, "LDS layout");
+static_assert(NLOAD <= 4 && NCOMP == 4, "landed and prog are read as one 16-byte word");
 
 struct PArgs {
     const q3_layer* layers;
@@ -164,14 +181,14 @@ __device__ __forceinline__ KArgs* uni_ptr(KArgs* p) {
 
 // Layer l's pointer table, read through the constant address space (scalar
 // loads): it is read-only for the whole launch, and a vector load of it would
-// make the streamers wait for every weight load in flight.
+// make the loaders wait for every weight load in flight.
 typedef const __attribute__((address_space(4))) q3_layer KLayer;
 __device__ __forceinline__ KLayer& layer(KArgs& a, int l) { return ((KLayer*)a.layers)[l]; }
 
 // The workgroup's LDS (one workgroup per CU).  A file-scope __shared__ object,
 // so helpers address it as LDS (ds_* instructions) rather than through generic
 // pointers, which would also count on the vector-memory counter.
-__shared__ Smem g_sm;
+__shared__ __align__(16) Smem g_sm;
 
 struct MatPart {
     int K, rb, re;
@@ -278,13 +295,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-// -------------------------------------------------------------- streamers
-
-// f(integral_constant<int, I>) for I = 0..N-1, expanded in source order.
-template <typename F, int... I>
-__device__ __forceinline__ void for_slots(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
+// ------------------------------------------------------ loaders and compute
 
 // A value every lane holds equally, moved to a scalar register so that the
 // branches on it are scalar branches (LDS reads land in vector registers).
@@ -309,7 +320,7 @@ struct SpinBound {
             t0 = now;
             return true;
         }
-        return now - t0 <= limit;
+        return uni(now - t0 <= limit ? 1 : 0) != 0;  // a scalar branch: the clock is the same in every lane
     }
 };
 
@@ -326,115 +337,194 @@ __device__ __forceinline__ bool wait_ready(int mi) {
     return true;
 }
 
-__device__ void streamer(KArgs* ka, int s, int lane) {
-    KArgs& a = *uni_ptr(ka);
-    s = uni(s);  // arguments arrive in vector registers
-    const int last = 4 * a.L;
+// LDS accesses of the loader waves, as inline assembly: the compiler cannot
+// tell them apart from the ring slots its own direct-to-LDS loads are writing,
+// and would otherwise wait for every load in flight before each of them.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ int lds_load_asm(const int* p) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return uni(v);
+}
+// Four counters at once (16-byte aligned).
+__device__ __forceinline__ u32x4_t lds_load4_asm(const int* p) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+__device__ __forceinline__ void lds_store_asm(int* p, int v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
+// s_waitcnt vmcnt(n) with the other counters left open (gfx9 encoding).
+#define Q3_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
-    // Issue cursor: the next unit to load.  Past the end it keeps re-reading the
-    // last unit, so every slot of the ring always holds exactly one load.
-    int imi = -1, irow = 0, ire = 0, ich = 0, ikc = 1;
-    int iK = 0;
-    bool iexh = false;
-    const bf16_t* ip = a.embed + lane * 8;
-    auto inext = [&]() {
-        for (int mi = imi + 1; mi <= last; ++mi) {
-            const int kind = mat_kind(mi, a.L);
-            const int row = uni(g_sm.prb[kind]) + s, re = uni(g_sm.pre[kind]);
-            if (row < re) {
-                const int K = uni(g_sm.pK[kind]);
-                imi = uni(mi); irow = uni(row); ire = uni(re); ich = 0; ikc = uni(K / CHUNK); iK = uni(K);
-                ip = mat_w(a, mi) + (int64_t)row * K + lane * 8;
-                return;
-            }
+// s_waitcnt vmcnt(n) for a run-time n in [0, N].
+template <int N>
+__device__ __forceinline__ void wait_vm_le(int n) {
+    if constexpr (N == 0) {
+        Q3_WAIT_VM(0);
+    } else {
+        if (n >= N) {
+            Q3_WAIT_VM(N);
+            return;
         }
-        iexh = true;
-    };
-    // Load the unit at the cursor into `reg`, advancing the cursor first so the
-    // load is the last instruction: the load must write the ring register
-    // itself (a copy out of a temporary would wait for every newer load).
-    auto issue = [&](u32x4_t& reg) {
-        const bf16_t* p = ip;
-        if (!iexh) {
-            ich = uni(ich + 1);
-            if (ich < ikc) {
-                ip += CHUNK;
-            } else {
-                ich = 0;
-                irow = uni(irow + NS);
-                if (irow < ire) ip += CHUNK + (int64_t)(NS - 1) * iK;
-                else inext();
-            }
-        }
-        reg = ldg_nt(p);
-    };
-
-    // Consume cursor: the unit in the oldest slot.
-    int cmi = -1, crow = 0, cre = 0, crb = 0, cch = 0, ckc = 1;
-    float acc = 0.f;
-    bool cfin = false;
-    auto signal = [&]() {
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        // Branch-free (every lane adds, lane 0 adds 1): a divergent branch here
-        // would make the structurizer mask the surrounding uniform control flow.
-        __hip_atomic_fetch_add(&g_sm.done, lane == 0 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    };
-    uint64_t* str = nullptr;  // streamer-0 trace: (wait began, input seen) per matrix
-    {
-        const int ts = trace_slot(uni(blockIdx.x), uni(gridDim.x));
-        if (a.trace && ts >= 0 && s == 0)
-            str = a.trace + (size_t)ts * (trace_words(a.L) / TRACE_WGS) + (a.L + 1) * TRACE_EV;
+        wait_vm_le<N - 1>(n);
     }
-    auto cnext = [&]() {
-        for (int mi = cmi + 1; mi <= last; ++mi) {
-            if (str) str[2 * mi] = wall_clock64();
-            if (!wait_ready(mi)) { cfin = true; return; }
-            if (str) str[2 * mi + 1] = wall_clock64();
-            const int kind = mat_kind(mi, a.L);
-            const int rb = uni(g_sm.prb[kind]), row = rb + s, re = uni(g_sm.pre[kind]);
-            if (row < re) {
-                cmi = uni(mi); crow = uni(row); cre = uni(re); crb = uni(rb); cch = 0;
-                ckc = uni(uni(g_sm.pK[kind]) / CHUNK);
-                return;
-            }
-            signal();  // no rows of this matrix for this wave
-        }
-        cfin = true;
-    };
+}
 
-    // One ring slot: consume the oldest unit, refill its register with the next
-    // load.  Slots are expanded with constant indices (a fold over an index
-    // sequence), so the ring stays in registers.
-    // Every slot refills its register unconditionally (past the end of the
-    // stream it re-reads the last unit): the compiler's wait counting then sees
-    // the same loads on every path and waits for exactly the slot being used.
-    auto step = [&](u32x4_t& reg) {
-        if (!cfin) {
-            const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(g_sm.x + cch * CHUNK + lane * 8);
-            acc = dot8v(reg, xv, acc);
-            cch = uni(cch + 1);
-            if (cch == ckc) {
-                const float t = wave_sum(acc);
-                g_sm.rows[crow - crb] = t;  // every lane holds t: branch-free store
-                acc = 0.f;
-                cch = 0;
-                crow = uni(crow + NS);
-                if (crow >= cre) {
-                    signal();
-                    cnext();
+// Weight units of this workgroup for the whole step, in order, into the LDS
+// ring: loader w takes units w, w + NLOAD, ... of the step's stream (every
+// matrix's rows [rb, re), each row's 512-element chunks in order).  A unit goes
+// out once its slot's previous unit has been consumed (every compute wave's
+// progress past it); the wave keeps LDEPTH loads in flight and publishes how
+// many of its units have landed.  The row partition comes from the kernel
+// arguments, not from LDS: after the first ring load, any LDS read the
+// compiler sees would wait for every load in flight.
+__device__ void loader(KArgs* ka, int w, int lane) {
+    KArgs& a = *uni_ptr(ka);
+    w = uni(w);
+    const int last = 4 * a.L;
+    int issued = 0;  // units issued
+    int outs = 0;    // of those, possibly still in flight (the last `outs`)
+    int minp = 0;    // cached min of the compute waves' progress
+    auto min_prog = [&]() {
+        const u32x4_t v = lds_load4_asm(g_sm.prog);
+        return uni(min(min((int)v.x, (int)v.y), min((int)v.z, (int)v.w)));
+    };
+    // Trace (loader 0): polls of a full ring per layer, in the all-workgroup
+    // trace; in the traced workgroups, when each matrix's first unit went out.
+    uint64_t* tra = a.trace && w == 0 ? a.trace + trace_words(a.L) : nullptr;
+    uint64_t* tri = nullptr;
+    if (tra && trace_slot(blockIdx.x, gridDim.x) >= 0)
+        tri = a.trace + (size_t)trace_slot(blockIdx.x, gridDim.x) * (trace_words(a.L) / TRACE_WGS) +
+              (a.L + 1) * TRACE_EV + 2 * (4 * a.L + 1);
+    int polls = 0;
+    int u = 0;  // stream index of the current matrix's first unit
+    for (int mi = 0; mi <= last; ++mi) {
+        const MatPart mp = mat_part(a, mat_kind(mi, a.L), blockIdx.x, gridDim.x);
+        const int kc = mp.K / CHUNK;
+        const int n = uni((mp.re - mp.rb) * kc);
+        const bf16_t* base = mat_w(a, mi) + (int64_t)mp.rb * mp.K + lane * 8;
+        if (tri) tri[mi] = wall_clock64();
+        for (int i = uni((w - u % NLOAD + NLOAD) % NLOAD); i < n; i += NLOAD) {
+            const int gu = u + i;
+            if (gu - RU >= minp) {
+                // The slot still holds an unconsumed unit: while waiting,
+                // publish this wave's loads one by one as they land (the
+                // consumers may be waiting for exactly those).
+                SpinBound sb;
+                while (gu - RU >= (minp = min_prog())) {
+                    ++polls;
+                    if (outs > 0) {
+                        --outs;
+                        wait_vm_le<LDEPTH>(outs);
+                        lds_store_asm(&g_sm.landed[w], issued - outs);
+                        continue;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    if (lds_load_asm(&g_sm.abort) || !sb.ok(STREAM_TIMEOUT)) {
+                        lds_store_asm(&g_sm.abort, 1);
+                        return;
+                    }
                 }
             }
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base + (int64_t)i * CHUNK),
+                                             (__attribute__((address_space(3))) void*)&g_sm.ring[(gu % RU) * 64],
+                                             16, 0, 2 /* non-temporal */);
+            issued = uni(issued + 1);
+            if (++outs > LDEPTH) {
+                Q3_WAIT_VM(LDEPTH);
+                outs = LDEPTH;
+                lds_store_asm(&g_sm.landed[w], issued - LDEPTH);
+            }
+            outs = uni(outs);
         }
-        // Keep the refill below the product that consumes the slot.
-        __builtin_amdgcn_sched_barrier(0);
-        issue(reg);
-    };
+        u = uni(u + n);
+        if (tra && (mi & 3) == 3 && mi < last) {
+            tra[((size_t)(mi >> 2) * gridDim.x + blockIdx.x) * TRACE_ALL + 6] = polls;
+            polls = 0;
+        }
+    }
+    Q3_WAIT_VM(0);
+    lds_store_asm(&g_sm.landed[w], issued);
+}
 
-    inext();
-    u32x4_t r[RING];
-    for_slots([&](auto i) { issue(r[decltype(i)::value]); }, std::make_integer_sequence<int, RING>{});
-    cnext();
-    while (!cfin) for_slots([&](auto i) { step(r[decltype(i)::value]); }, std::make_integer_sequence<int, RING>{});
+// Every unit of the stream below the returned index has landed in the ring
+// (loader w's first landed[w] units are w, w + NLOAD, ...).
+__device__ __forceinline__ int landed_below() {
+    const u32x4_t v = lds_load4_asm(g_sm.landed);
+    const int n[4] = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+    int m = 0x7fffffff;
+#pragma unroll
+    for (int w = 0; w < NLOAD; ++w) m = min(m, w + NLOAD * n[w]);
+    return uni(m);
+}
+
+// Compute wave c: for every matrix, once its input is staged, the dot products
+// of rows rb + c, rb + c + NCOMP, ... with x.  A row is taken once all its
+// units have landed; its chunks are read from the ring in order and summed per
+// lane, then across the wave -- the arithmetic and order of the GEMV kernel
+// (q3_gemv).  prog[c] then moves to the first unit of the wave's next row.
+__device__ void compute(KArgs* ka, int c, int lane) {
+    KArgs& a = *uni_ptr(ka);
+    c = uni(c);
+    const int last = 4 * a.L;
+    const int ulayer = uni(g_sm.ulayer);
+    int bound = 0;  // cached landed_below()
+    uint64_t* tra = a.trace && c == 0 ? a.trace + trace_words(a.L) : nullptr;
+    int polls = 0;  // trace: polls for landed units per layer (compute wave 0)
+    uint64_t* tr = nullptr;  // compute wave 0's input waits, in the traced workgroups
+    if (a.trace && c == 0 && trace_slot(blockIdx.x, gridDim.x) >= 0)
+        tr = a.trace + (size_t)trace_slot(blockIdx.x, gridDim.x) * (trace_words(a.L) / TRACE_WGS) + (a.L + 1) * TRACE_EV;
+    for (int mi = 0; mi <= last; ++mi) {
+        if (tr) tr[2 * mi] = wall_clock64();
+        if (!wait_ready(mi)) return;
+        if (tr) tr[2 * mi + 1] = wall_clock64();
+        const int kind = mat_kind(mi, a.L);
+        const int K = uni(g_sm.pK[kind]), rb = uni(g_sm.prb[kind]), re = uni(g_sm.pre[kind]);
+        const int kc = K / CHUNK;
+        const int base = (mi == last ? a.L * ulayer : (mi >> 2) * ulayer) + uni(g_sm.poff[kind]);
+        const int next = mi == last ? 0x7fffffff
+                       : mi + 1 == last ? a.L * ulayer + uni(g_sm.poff[M_LM])
+                       : ((mi + 1) >> 2) * ulayer + uni(g_sm.poff[mat_kind(mi + 1, a.L)]);
+        for (int r = rb + c; r < re; r += NCOMP) {
+            const int u0 = uni(base + (r - rb) * kc);
+            if (bound < u0 + kc) {
+                SpinBound sb;
+                while ((bound = landed_below()) < u0 + kc) {
+                    ++polls;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (!sb.ok(STREAM_TIMEOUT)) {
+                        __hip_atomic_store(&g_sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        return;
+                    }
+                }
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            }
+            float acc = 0.f;
+            int slot = u0 % RU;
+#pragma unroll 4
+            for (int ch = 0; ch < kc; ++ch) {
+                const u32x4_t wv = g_sm.ring[slot * 64 + lane];
+                const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(g_sm.x + ch * CHUNK + lane * 8);
+                acc = dot8v(wv, xv, acc);
+                slot = slot + 1 == RU ? 0 : slot + 1;
+            }
+            g_sm.rows[r - rb] = wave_sum(acc);  // every lane holds the sum: branch-free store
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __hip_atomic_store(&g_sm.prog[c], r + NCOMP < re ? u0 + NCOMP * kc : next, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __hip_atomic_store(&g_sm.prog[c], next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_add(&g_sm.done, lane == 0 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (tra && (mi & 3) == 3 && mi < last) {
+            tra[((size_t)(mi >> 2) * gridDim.x + blockIdx.x) * TRACE_ALL + 7] = polls;
+            polls = 0;
+        }
+    }
 }
 
 // ----------------------------------------------------------------- control
@@ -487,7 +577,7 @@ __device__ __forceinline__ void publish(Ctl& c) {
 }
 
 __device__ bool wait_done(Ctl& c) {
-    const int target = c.staged * NS;
+    const int target = c.staged * NCOMP;
     auto done = []() { return uni(__hip_atomic_load(&g_sm.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)); };
     SpinBound sb;
     while (done() < target) {
@@ -1090,19 +1180,27 @@ __global__ __launch_bounds__(PTHREADS) void decode_persist_kernel(PArgs args) {
     (void)args;  // read in place through the kernarg segment
     KArgs* ka = (KArgs*)(__builtin_amdgcn_kernarg_segment_ptr());
     const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (threadIdx.x < 5) {
-        const MatPart p = mat_part(*ka, threadIdx.x, blockIdx.x, gridDim.x);
-        g_sm.pK[threadIdx.x] = p.K;
-        g_sm.prb[threadIdx.x] = p.rb;
-        g_sm.pre[threadIdx.x] = p.re;
-    }
     if (threadIdx.x == 0) {
+        int off = 0;
+        for (int k = 0; k < 5; ++k) {
+            const MatPart p = mat_part(*ka, k, blockIdx.x, gridDim.x);
+            g_sm.pK[k] = p.K;
+            g_sm.prb[k] = p.rb;
+            g_sm.pre[k] = p.re;
+            if (k == M_LM) off = 0;  // the LM head follows the last layer
+            g_sm.poff[k] = off;
+            off += (p.re - p.rb) * (p.K / CHUNK);
+            if (k == M_DOWN) g_sm.ulayer = off;
+        }
+        for (int w = 0; w < NLOAD; ++w) g_sm.landed[w] = 0;
+        for (int c = 0; c < NCOMP; ++c) g_sm.prog[c] = 0;
         g_sm.ready = 0;
         g_sm.done = 0;
         g_sm.abort = 0;
     }
     __syncthreads();
-    if (wave < NS) streamer(ka, wave, lane);
+    if (wave < NLOAD) loader(ka, wave, lane);
+    else if (wave < CTL_WAVE) compute(ka, wave - NLOAD, lane);
     else control(ka, lane, blockIdx.x, gridDim.x);
 }
 
