@@ -62,7 +62,10 @@ constexpr int NLOAD = 3;              // loader waves 0..2: weights HBM -> LDS r
 constexpr int NCOMP = 4;              // compute waves 3..6: ring x input -> row sums
 constexpr int CTL_WAVE = NLOAD + NCOMP;  // wave 7: exchange, norms, epilogues, attention
 static_assert(CTL_WAVE == NWAVES - 1, "wave roles");
-constexpr int RU = 96;                // ring units (1 KB each) in LDS
+#ifndef Q3_PERSIST_RU
+#define Q3_PERSIST_RU 96
+#endif
+constexpr int RU = Q3_PERSIST_RU;     // ring units (1 KB each) in LDS
 #ifndef Q3_PERSIST_LDEPTH
 #define Q3_PERSIST_LDEPTH 8
 #endif
@@ -133,7 +136,7 @@ struct Smem {
     __align__(16) int landed[4];  // per loader wave: its units (every NLOAD-th) landed in the ring
     __align__(16) int prog[4];    // per compute wave: every unit of its below this index consumed
     int ready;                // matrices whose input is staged (control -> compute waves)
-    int done;                 // (compute wave, matrix) completions (compute waves -> control)
+    int done;                 // 64 x (compute wave, matrix) completions (compute waves -> control)
     int abort;
 };
 static_assert(sizeof(Smem) <= LDS_BYTES, "LDS layout");
@@ -312,11 +315,12 @@ constexpr uint32_t CLOCK_EVERY = 1024;
 struct SpinBound {
     uint64_t t0 = 0;
     uint32_t it = 0;
-    // False once `limit` wall-clock ticks have passed since the first call.
+    // False once `limit` wall-clock ticks have passed since the CLOCK_EVERY-th
+    // call (short waits never read the clock).
     __device__ __forceinline__ bool ok(uint64_t limit) {
-        if ((it++ % CLOCK_EVERY) != 0) return true;
+        if ((++it % CLOCK_EVERY) != 0) return true;
         const uint64_t now = wall_clock64();
-        if (it == 1) {
+        if (it == CLOCK_EVERY) {
             t0 = now;
             return true;
         }
@@ -327,7 +331,7 @@ struct SpinBound {
 __device__ __forceinline__ bool wait_ready(int mi) {
     SpinBound sb;
     while (lds_ready() <= mi) {
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);
         if (!sb.ok(STREAM_TIMEOUT)) {
             __hip_atomic_store(&g_sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             return false;
@@ -519,7 +523,8 @@ __device__ void compute(KArgs* ka, int c, int lane) {
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __hip_atomic_store(&g_sm.prog[c], next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        __hip_atomic_fetch_add(&g_sm.done, lane == 0 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        // Every lane adds 1 (a uniform operand: one ds_add of 64, no loop over lanes).
+        __hip_atomic_fetch_add(&g_sm.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (tra && (mi & 3) == 3 && mi < last) {
             tra[((size_t)(mi >> 2) * gridDim.x + blockIdx.x) * TRACE_ALL + 7] = polls;
             polls = 0;
@@ -577,7 +582,7 @@ __device__ __forceinline__ void publish(Ctl& c) {
 }
 
 __device__ bool wait_done(Ctl& c) {
-    const int target = c.staged * NCOMP;
+    const int target = c.staged * NCOMP * Q3_WAVE;  // each compute wave adds 64 per matrix
     auto done = []() { return uni(__hip_atomic_load(&g_sm.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)); };
     SpinBound sb;
     while (done() < target) {
@@ -651,6 +656,14 @@ __device__ __attribute__((noinline)) bool stage_norm(Ctl c, const uint32_t* src_
     c.scalarize();
     constexpr int MC = 8;
     const int n8 = K / 8;
+    // The gain does not depend on the exchange: its loads go out first.
+    uint4 gv[MC];
+#pragma unroll
+    for (int m = 0; m < MC; ++m)
+        if (c.lane + 64 * m < n8) {
+            const u32x4_t t = ldg(gain + (c.lane + 64 * m) * 8);
+            gv[m] = make_uint4(t.x, t.y, t.z, t.w);
+        }
     uint4 xv[MC];
     if (src_plain) {
 #pragma unroll
@@ -667,13 +680,6 @@ __device__ __attribute__((noinline)) bool stage_norm(Ctl c, const uint32_t* src_
             xv[m] = make_uint4(bfpair(lo[m].x, lo[m].y), bfpair(lo[m].z, lo[m].w), bfpair(hi[m].x, hi[m].y),
                                bfpair(hi[m].z, hi[m].w));
     }
-    uint4 gv[MC];
-#pragma unroll
-    for (int m = 0; m < MC; ++m)
-        if (c.lane + 64 * m < n8) {
-            const u32x4_t t = ldg(gain + (c.lane + 64 * m) * 8);
-            gv[m] = make_uint4(t.x, t.y, t.z, t.w);
-        }
     float ss[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < MC; ++m) {
@@ -751,24 +757,20 @@ __device__ __attribute__((noinline)) void gather_kv(const bf16_t* kb, const bf16
 
 // Per-head RMSNorm + RoPE of a 128-wide row spread over the 16 lanes of each
 // lane row (lane holds dims 8 (l % 16) .. +8; dims d and d + 64 are 8 lanes
-// apart).  t = bf16(x * rsqrt(mean(x^2) + eps)); y = bf16(w * t); then
+// apart); g, cv, sv are this lane's 8 gains, cosines and sines.  t = bf16(x * rsqrt(mean(x^2) + eps)); y = bf16(w * t); then
 // lo' = bf16(bf16(lo c) + bf16(-hi s)), hi' = bf16(bf16(hi c) + bf16(lo s))
 // (reference fused.py:196-219, engine.py:91-109).
-__device__ __forceinline__ u32x4_t norm_rope8(u32x4_t x, const bf16_t* gain, const bf16_t* cosr,
-                                             const bf16_t* sinr, float eps, int lane) {
+__device__ __forceinline__ u32x4_t norm_rope8(u32x4_t x, u32x4_t g, u32x4_t cv, u32x4_t sv, float eps, int lane) {
     const int d0 = (lane & 15) * 8;
     float f[8] = {bflo(x.x), bfhi(x.x), bflo(x.y), bfhi(x.y), bflo(x.z), bfhi(x.z), bflo(x.w), bfhi(x.w)};
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
     const float inv = inv_rms(row16_dpp(ss), PD, eps);
-    const u32x4_t g = ldg(gain + d0);
     const float gf[8] = {bflo(g.x), bfhi(g.x), bflo(g.y), bfhi(g.y), bflo(g.z), bfhi(g.z), bflo(g.w), bfhi(g.w)};
     float n[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) n[e] = bf2f(norm_elem(f[e], inv, gf[e]));
-    const u32x4_t cv = ldg(cosr + d0);
-    const u32x4_t sv = ldg(sinr + d0);
     const float cf[8] = {bflo(cv.x), bfhi(cv.x), bflo(cv.y), bfhi(cv.y), bflo(cv.z), bfhi(cv.z), bflo(cv.w), bfhi(cv.w)};
     const float sf[8] = {bflo(sv.x), bfhi(sv.x), bflo(sv.y), bfhi(sv.y), bflo(sv.z), bfhi(sv.z), bflo(sv.w), bfhi(sv.w)};
     const bool low = (lane & 8) == 0;  // dims < 64
@@ -828,6 +830,13 @@ __device__ __attribute__((noinline)) bool attention(Ctl c, int l, AttnPlan p) {
     const int koff = (qsz + p.h * PD + d0) * 4;
     const int voff = (qsz + a.Hkv * PD + p.h * PD + d0) * 4;
     const uint32_t F = c.flag(l, OP_QKV);
+    // The gains and this position's cos / sin do not depend on the exchange:
+    // their loads go out first and land while the q / k / v rows are awaited.
+    KLayer& ly = layer(a, l);
+    const bf16_t* cosr = a.cos_t + (int64_t)c.pos * PD;
+    const bf16_t* sinr = a.sin_t + (int64_t)c.pos * PD;
+    const u32x4_t gq = ldg(ly.q_norm + d0), gk = ldg(ly.k_norm + d0);
+    const u32x4_t cv = ldg(cosr + d0), sv = ldg(sinr + d0);
     u32x4_t w[6];
     const uint32_t Fs = F << 16;
     Deadline dl;
@@ -844,9 +853,6 @@ __device__ __attribute__((noinline)) bool attention(Ctl c, int l, AttnPlan p) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     c.mark(l, T_ATT_IN);
     c.mark_all(l, 1);
-    KLayer& ly = layer(a, l);
-    const bf16_t* cosr = a.cos_t + (int64_t)c.pos * PD;
-    const bf16_t* sinr = a.sin_t + (int64_t)c.pos * PD;
     u32x4_t qv, kn, vn;
     qv.x = bfpair(w[0].x, w[0].y); qv.y = bfpair(w[0].z, w[0].w);
     qv.z = bfpair(w[1].x, w[1].y); qv.w = bfpair(w[1].z, w[1].w);
@@ -854,8 +860,8 @@ __device__ __attribute__((noinline)) bool attention(Ctl c, int l, AttnPlan p) {
     kn.z = bfpair(w[3].x, w[3].y); kn.w = bfpair(w[3].z, w[3].w);
     vn.x = bfpair(w[4].x, w[4].y); vn.y = bfpair(w[4].z, w[4].w);
     vn.z = bfpair(w[5].x, w[5].y); vn.w = bfpair(w[5].z, w[5].w);
-    const u32x4_t qr = norm_rope8(qv, ly.q_norm, cosr, sinr, a.eps, lane);
-    kn = norm_rope8(kn, ly.k_norm, cosr, sinr, a.eps, lane);
+    const u32x4_t qr = norm_rope8(qv, gq, cv, sv, a.eps, lane);
+    kn = norm_rope8(kn, gk, cv, sv, a.eps, lane);
     if (p.owner && g == 0) {
         // This token's K and V into the cache (fused.py:553-617); later steps read them.
         const int64_t off = (int64_t)c.pos * PD + d0;
