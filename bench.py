@@ -197,13 +197,17 @@ def main() -> int:
     for _ in range(W):
         eng._decode_step()
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(eng.stream)
-    for _ in range(K):
+    # One event between consecutive replays: the mean over the K steps is the
+    # headline, the median of the per-step durations is reported beside it.
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    events[0].record(eng.stream)
+    for k in range(K):
         eng._decode_step()
-    stop.record(eng.stream)
+        events[k + 1].record(eng.stream)
     torch.cuda.synchronize()
-    ms_step = start.elapsed_time(stop) / K
+    ms_step = events[0].elapsed_time(events[K]) / K
+    per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(K))
+    ms_median = per_step[K // 2] if K % 2 else 0.5 * (per_step[K // 2 - 1] + per_step[K // 2])
     value = B * K / (ms_step * K / 1e3)
 
     wbytes = weight_bytes(eng)
@@ -230,6 +234,7 @@ def main() -> int:
         "steps": K,
         "warmup": W,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(ms_median, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -134,11 +134,10 @@ __device__ __forceinline__ void argmax_epilogue(const SkinnyArgs& a, const f32x4
     }
 }
 
-// NCH chunks per split, fully unrolled: weight loads run two chunks ahead in a
-// three-slot register ring, x one chunk ahead through a double-buffered LDS
-// tile.  Loads are issued x(c+1) then W(c+2), so storing x(c+1) waits only for
-// loads issued before it and W(c+2) stays in flight (vector memory counters
-// retire in order).
+// NCH chunks per split, fully unrolled: weight loads run WA chunks ahead in a
+// register ring, x XA chunks ahead (registers, then a double-buffered LDS
+// tile).  Storing x(c+1) waits only for the loads issued before it; the later
+// weight and x loads stay in flight (vector memory counters retire in order).
 template <int MT, int NCH, bool TILED>
 __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
     __shared__ __align__(16) bf16_t xs[2][16 * MT * KC];
@@ -168,24 +167,32 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint4 w[3][8], xr[MT * 2];
-    load_x<MT>(a, kbeg, xr);
-    if (active) load(kbeg, w[0]);
-    if (active && kbeg + KC < kend) load(kbeg + KC, w[1]);
-    store_x<MT>(xs[0], xr);
+    // Weights run WA chunks ahead in a register ring, x XA chunks ahead in
+    // register sets (its LDS tile is double-buffered).  With few batch tiles
+    // the registers allow the deeper prefetch; at MT >= 3 it would cost
+    // occupancy.
+    constexpr int WA = MT <= 2 ? 3 : 2, XA = 2;
+    uint4 w[WA + 1][8], xr[XA][MT * 2];
+#pragma unroll
+    for (int i = 0; i < XA; ++i)
+        if (kbeg + i * KC < kend) load_x<MT>(a, kbeg + i * KC, xr[i]);
+#pragma unroll
+    for (int i = 0; i < WA; ++i)
+        if (active && kbeg + i * KC < kend) load(kbeg + i * KC, w[i]);
+    store_x<MT>(xs[0], xr[0]);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int k0 = kbeg + c * KC;
         if (k0 < kend) {
-            const bool nx = k0 + KC < kend;
-            if (nx) load_x<MT>(a, k0 + KC, xr);
-            if (active && k0 + 2 * KC < kend) load(k0 + 2 * KC, w[(c + 2) % 3]);
+            // x(c) is in LDS, so its register set takes x(c + XA).
+            if (k0 + XA * KC < kend) load_x<MT>(a, k0 + XA * KC, xr[c % XA]);
+            if (active && k0 + WA * KC < kend) load(k0 + WA * KC, w[(c + WA) % (WA + 1)]);
             if (active) {
                 const bf16_t* xb = xs[c & 1];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const bf16x8_t av = as_bf16x8(w[c % 3][j]);
+                    const bf16x8_t av = as_bf16x8(w[c % (WA + 1)][j]);
                     const int ch = 4 * j + g;  // 16-byte chunk of the x row
 #pragma unroll
                     for (int t = 0; t < MT; ++t) {
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
                     }
                 }
             }
-            if (nx) store_x<MT>(xs[(c + 1) & 1], xr);
+            if (k0 + KC < kend) store_x<MT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
             __syncthreads();
         }
     }
