@@ -569,6 +569,16 @@ struct Ctl {
     }
 };
 
+// Ctl as scalar arguments of the noinline helpers: a struct argument would be
+// passed through scratch memory, and every call would wait for it.
+#define Q3_CTL_PARAMS                                                                                  \
+    KArgs *c_ka, uint64_t *c_tr, uint64_t *c_tra, int c_lane, int c_wg, int c_G, int c_pos, int64_t c_tok, \
+        uint32_t c_fbase, int c_staged
+#define Q3_CTL_ARGS(c) (c).ka, (c).tr, (c).tra, (c).lane, (c).wg, (c).G, (c).pos, (c).tok, (c).fbase, (c).staged
+#define Q3_CTL_MAKE                                                                \
+    Ctl c{c_ka, c_tr, c_tra, c_lane, c_wg, c_G, c_pos, c_tok, c_fbase, c_staged}; \
+    c.scalarize()
+
 __device__ void fail(Ctl& c, uint32_t code) {
     __hip_atomic_store(c.ka->state + 1, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (c.lane == 0) c.ka->tokens[0] = -1;
@@ -651,9 +661,9 @@ __device__ bool poll_chunks(Ctl& c, const uint32_t* base, int n8, int m0, uint32
 // then each 64-thread wave is reduced and the four wave sums are added as
 // (w0 + w1) + (w2 + w3).  Lane l plays threads l, l+64, l+128, l+192: its chunk
 // l + 64 m belongs to thread l + 64 (m % 4).
-__device__ __attribute__((noinline)) bool stage_norm(Ctl c, const uint32_t* src_x, uint32_t F, const bf16_t* src_plain,
+__device__ __attribute__((noinline)) bool stage_norm(Q3_CTL_PARAMS, const uint32_t* src_x, uint32_t F, const bf16_t* src_plain,
                            const bf16_t* gain, int K) {
-    c.scalarize();
+    Q3_CTL_MAKE;
     constexpr int MC = 8;
     const int n8 = K / 8;
     // The gain does not depend on the exchange: its loads go out first.
@@ -711,8 +721,8 @@ __device__ __attribute__((noinline)) bool stage_norm(Ctl c, const uint32_t* src_
 }
 
 // x = the flagged vector src (K elements) into LDS as BF16.
-__device__ __attribute__((noinline)) bool stage_plain(Ctl c, const uint32_t* src_x, uint32_t F, int K) {
-    c.scalarize();
+__device__ __attribute__((noinline)) bool stage_plain(Q3_CTL_PARAMS, const uint32_t* src_x, uint32_t F, int K) {
+    Q3_CTL_MAKE;
     const int n8 = K / 8;
     for (int m0 = 0; 64 * m0 < n8; m0 += STAGE_CHUNKS) {
         u32x4_t lo[STAGE_CHUNKS], hi[STAGE_CHUNKS];
@@ -819,8 +829,10 @@ __device__ AttnPlan attn_plan(const Ctl& c, int l) {
 // the cache by the range that holds it, then the online softmax over the cached
 // keys (first set prefetched by the caller) and the new key.  Publishes the
 // unnormalised partial (acc, m, l) of each of the 4 query heads.
-__device__ __attribute__((noinline)) bool attention(Ctl c, int l, AttnPlan p) {
-    c.scalarize();
+__device__ __attribute__((noinline)) bool attention(Q3_CTL_PARAMS, int l, int p_h, int p_s, int p_S, int p_k0, int p_k1, bool p_owner,
+                                                    const bf16_t* p_kb, const bf16_t* p_vb) {
+    Q3_CTL_MAKE;
+    const AttnPlan p{uni(p_h), uni(p_s), uni(p_S), uni(p_k0), uni(p_k1), uni(p_owner ? 1 : 0) != 0, p_kb, p_vb};
     KArgs& a = *c.ka;
     const int lane = c.lane, g = lane >> 4, d0 = (lane & 15) * 8;
     const int qsz = a.Hq * PD;
@@ -926,8 +938,8 @@ __device__ __attribute__((noinline)) bool attention(Ctl c, int l, AttnPlan p) {
 // This workgroup's slice of the split merge: outputs [o0, o0 + n) of the Hq*128
 // attention vector (one query head), out = bf16(sum_s acc_s e^(m_s - M) /
 // sum_s l_s e^(m_s - M)) over the key ranges that hold keys (fused.py:793-823).
-__device__ __attribute__((noinline)) bool merge(Ctl c, int l) {
-    c.scalarize();
+__device__ __attribute__((noinline)) bool merge(Q3_CTL_PARAMS, int l) {
+    Q3_CTL_MAKE;
     KArgs& a = *c.ka;
     const int lane = c.lane;
     const int T = a.Hq * PD;
@@ -1018,14 +1030,14 @@ __device__ __attribute__((noinline)) bool merge(Ctl c, int l) {
 
 // ------------------------------------------------------------- epilogues
 
-__device__ __attribute__((noinline)) void publish_rows(Ctl c, uint32_t* dst, int rb, int n, uint32_t F) {
-    c.scalarize();
+__device__ __attribute__((noinline)) void publish_rows(Q3_CTL_PARAMS, uint32_t* dst, int rb, int n, uint32_t F) {
+    Q3_CTL_MAKE;
     for (int i = c.lane; i < n; i += 64) st_coh32(dst + rb + i, word(f2bf(g_sm.rows[i]), F));
 }
 
 // resid = bf16(resid + bf16(row sum)) on this workgroup's residual rows (fused.py:135-138).
-__device__ __attribute__((noinline)) void publish_resid(Ctl c, int rb, int n, uint32_t F) {
-    c.scalarize();
+__device__ __attribute__((noinline)) void publish_resid(Q3_CTL_PARAMS, int rb, int n, uint32_t F) {
+    Q3_CTL_MAKE;
     for (int i = c.lane; i < n; i += 64) {
         const uint32_t v = f2bf(bf2f(g_sm.own[i]) + rbf(g_sm.rows[i]));
         g_sm.own[i] = (bf16_t)v;
@@ -1034,8 +1046,8 @@ __device__ __attribute__((noinline)) void publish_resid(Ctl c, int rb, int n, ui
 }
 
 // act[j] = bf16(bf16(silu(g)) * u) from the interleaved rows (gate_j, up_j) (fused.py:107-111).
-__device__ __attribute__((noinline)) void publish_swiglu(Ctl c, int rb, int n, uint32_t F) {
-    c.scalarize();
+__device__ __attribute__((noinline)) void publish_swiglu(Q3_CTL_PARAMS, int rb, int n, uint32_t F) {
+    Q3_CTL_MAKE;
     const int pb = rb / 2;
     for (int j = c.lane; j < n / 2; j += 64) {
         const float gte = rbf(g_sm.rows[2 * j]), up = rbf(g_sm.rows[2 * j + 1]);
@@ -1044,8 +1056,8 @@ __device__ __attribute__((noinline)) void publish_swiglu(Ctl c, int rb, int n, u
 }
 
 // (max BF16 logit, lowest index) of this workgroup's LM-head rows (engine.py:833).
-__device__ __attribute__((noinline)) void publish_argmax(Ctl c, int rb, int n, uint32_t F) {
-    c.scalarize();
+__device__ __attribute__((noinline)) void publish_argmax(Q3_CTL_PARAMS, int rb, int n, uint32_t F) {
+    Q3_CTL_MAKE;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int i = c.lane; i < n; i += 64) {
@@ -1069,8 +1081,8 @@ __device__ __attribute__((noinline)) void publish_argmax(Ctl c, int rb, int n, u
 }
 
 // Workgroup 0: the greedy token from every workgroup's partial; advances pos and the epoch.
-__device__ __attribute__((noinline)) bool finish(Ctl c, uint32_t epoch) {
-    c.scalarize();
+__device__ __attribute__((noinline)) bool finish(Q3_CTL_PARAMS, uint32_t epoch) {
+    Q3_CTL_MAKE;
     const uint32_t F = c.flag(c.ka->L, 0);
     const auto rs = rsrc(c.ka->lm_x);
     float bv = -INFINITY;
@@ -1131,8 +1143,8 @@ __device__ void control(KArgs* ka, int lane, int wg, int G) {
     for (int l = 0; l < a.L; ++l) {
         KLayer& ly = layer(a, l);
         // qkv = W_qkv . RMSNorm(resid)
-        const bool ok = l == 0 ? stage_norm(c, nullptr, 0, emb, ly.in_ln, a.H)
-                               : stage_norm(c, a.resid_x, c.flag(l - 1, OP_DOWN), nullptr, ly.in_ln, a.H);
+        const bool ok = l == 0 ? stage_norm(Q3_CTL_ARGS(c), nullptr, 0, emb, ly.in_ln, a.H)
+                               : stage_norm(Q3_CTL_ARGS(c), a.resid_x, c.flag(l - 1, OP_DOWN), nullptr, ly.in_ln, a.H);
         if (!ok) return;
         c.mark(l, T_QKV_IN);
         publish(c);
@@ -1142,44 +1154,44 @@ __device__ void control(KArgs* ka, int lane, int wg, int G) {
         if (!wait_done(c)) return;
         c.mark(l, T_QKV_DONE);
         c.mark_all(l, 0);
-        publish_rows(c, a.qkv_x, pq.rb, pq.re - pq.rb, c.flag(l, OP_QKV));
-        if (!attention(c, l, ap)) return;
+        publish_rows(Q3_CTL_ARGS(c), a.qkv_x, pq.rb, pq.re - pq.rb, c.flag(l, OP_QKV));
+        if (!attention(Q3_CTL_ARGS(c), l, ap.h, ap.s, ap.S, ap.k0, ap.k1, ap.owner, ap.kb, ap.vb)) return;
         c.mark(l, T_ATT_DONE);
         c.mark_all(l, 2);
-        if (!merge(c, l)) return;
+        if (!merge(Q3_CTL_ARGS(c), l)) return;
         c.mark(l, T_MRG_DONE);
         c.mark_all(l, 3);
         // resid += W_o . attn
-        if (!stage_plain(c, a.attn_x, c.flag(l, OP_MERGE), a.Hq * PD)) return;
+        if (!stage_plain(Q3_CTL_ARGS(c), a.attn_x, c.flag(l, OP_MERGE), a.Hq * PD)) return;
         c.mark(l, T_O_IN);
         publish(c);
         if (!wait_done(c)) return;
         c.mark(l, T_O_DONE);
-        publish_resid(c, po.rb, po.re - po.rb, c.flag(l, OP_O));
+        publish_resid(Q3_CTL_ARGS(c), po.rb, po.re - po.rb, c.flag(l, OP_O));
         // act = SwiGLU(W_gu . RMSNorm(resid))
-        if (!stage_norm(c, a.resid_x, c.flag(l, OP_O), nullptr, ly.post_ln, a.H)) return;
+        if (!stage_norm(Q3_CTL_ARGS(c), a.resid_x, c.flag(l, OP_O), nullptr, ly.post_ln, a.H)) return;
         c.mark(l, T_GU_IN);
         publish(c);
         if (!wait_done(c)) return;
         c.mark(l, T_GU_DONE);
-        publish_swiglu(c, pg.rb, pg.re - pg.rb, c.flag(l, OP_GU));
+        publish_swiglu(Q3_CTL_ARGS(c), pg.rb, pg.re - pg.rb, c.flag(l, OP_GU));
         // resid += W_down . act
-        if (!stage_plain(c, a.act_x, c.flag(l, OP_GU), a.I)) return;
+        if (!stage_plain(Q3_CTL_ARGS(c), a.act_x, c.flag(l, OP_GU), a.I)) return;
         c.mark(l, T_DN_IN);
         publish(c);
         if (!wait_done(c)) return;
         c.mark(l, T_DN_DONE);
-        publish_resid(c, pd.rb, pd.re - pd.rb, c.flag(l, OP_DOWN));
+        publish_resid(Q3_CTL_ARGS(c), pd.rb, pd.re - pd.rb, c.flag(l, OP_DOWN));
     }
     // token = argmax(E . RMSNorm(resid))
-    if (!stage_norm(c, a.resid_x, c.flag(a.L - 1, OP_DOWN), nullptr, a.final_norm, a.H)) return;
+    if (!stage_norm(Q3_CTL_ARGS(c), a.resid_x, c.flag(a.L - 1, OP_DOWN), nullptr, a.final_norm, a.H)) return;
     c.mark(a.L, T_QKV_IN);
     publish(c);
     if (!wait_done(c)) return;
     c.mark(a.L, T_QKV_DONE);
     const MatPart pl = mat_part(a, M_LM, c.wg, c.G);
-    publish_argmax(c, pl.rb, pl.re - pl.rb, c.flag(a.L, 0));
-    if (wg == 0) finish(c, epoch);
+    publish_argmax(Q3_CTL_ARGS(c), pl.rb, pl.re - pl.rb, c.flag(a.L, 0));
+    if (wg == 0) finish(Q3_CTL_ARGS(c), epoch);
 }
 
 __global__ __launch_bounds__(PTHREADS) void decode_persist_kernel(PArgs args) {
