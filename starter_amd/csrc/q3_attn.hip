@@ -519,16 +519,16 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
     const long groups = (long)splits * Hkv * B;
     const int per = split_len(capacity, splits);
     if (groups <= 256 && per >= 8 * BLK)
-        hipLaunchKernelGGL(attn_decode_kernel<8>, dim3(splits, Hkv, B), dim3(8 * 64), 0, stream, a);
+        Q3_LAUNCH(attn_decode_kernel<8>, dim3(splits, Hkv, B), dim3(8 * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL(attn_decode_kernel<4>, dim3(splits, Hkv, B), dim3(4 * 64), 0, stream, a);
+        Q3_LAUNCH(attn_decode_kernel<4>, dim3(splits, Hkv, B), dim3(4 * 64), 0, stream, a);
     Q3_CHECK_LAUNCH();
 }
 
 extern "C" int q3_attn_merge(const float* part_acc, const float* part_ml, bf16_t* out, int B, int Hq,
                              int splits, hipStream_t stream) {
     if (B < 1 || Hq < 1 || splits < 1) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(Hq, B), dim3(D), 0, stream, part_acc, part_ml, out, Hq, splits);
+    Q3_LAUNCH(attn_merge_kernel, dim3(Hq, B), dim3(D), 0, stream, part_acc, part_ml, out, Hq, splits);
     Q3_CHECK_LAUNCH();
 }
 
@@ -536,7 +536,7 @@ extern "C" int q3_attn_prefill(const bf16_t* q, const bf16_t* cache_k, const bf1
                                int B, int T, int start, int Hq, int Hkv, int capacity, float scale,
                                hipStream_t stream) {
     if (B < 1 || T < 1 || start < 0 || Hq != GROUP * Hkv || start + T > capacity) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3((T + 31) / 32, Hkv, B), dim3(THREADS), 0, stream,
+    Q3_LAUNCH(attn_prefill_kernel, dim3((T + 31) / 32, Hkv, B), dim3(THREADS), 0, stream,
                        q, cache_k, cache_v, out, T, start, Hq, Hkv, capacity, scale);
     Q3_CHECK_LAUNCH();
 }

@@ -116,4 +116,12 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
 // then one rounding (reference fused.py:107-111).
 __device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + expf(-g))); }
 
+// hipGetLastError reports the last error of any runtime call on this thread,
+// so each launch first clears it: the check after the launch then reports
+// that launch, not a stale code an unrelated (already handled) call left.
+#define Q3_LAUNCH(...)                   \
+    do {                                 \
+        (void)hipGetLastError();         \
+        hipLaunchKernelGGL(__VA_ARGS__); \
+    } while (0)
 #define Q3_CHECK_LAUNCH() return (int)hipGetLastError()

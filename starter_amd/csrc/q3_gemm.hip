@@ -141,15 +141,15 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     switch (epi) {
         case Q3_EPI_STORE:
-            hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, Q3_EPI_STORE>), grid, dim3(THREADS), 0, stream, x,
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_STORE>), grid, dim3(THREADS), 0, stream, x,
                                ldx, w, M, N, K, y, ldy);
             break;
         case Q3_EPI_RESID:
-            hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, Q3_EPI_RESID>), grid, dim3(THREADS), 0, stream, x,
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_RESID>), grid, dim3(THREADS), 0, stream, x,
                                ldx, w, M, N, K, y, ldy);
             break;
         case Q3_EPI_SWIGLU:
-            hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, Q3_EPI_SWIGLU>), grid, dim3(THREADS), 0, stream, x,
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_SWIGLU>), grid, dim3(THREADS), 0, stream, x,
                                ldx, w, M, N, K, y, ldy);
             break;
         default:

@@ -353,7 +353,7 @@ int launch_one(const GemvArgs& a, hipStream_t stream) {
     if (a.N % R != 0) return -1;
     const int blocks = (a.N / R + GEMV_WAVES - 1) / GEMV_WAVES;
     const size_t shmem = XLDS ? (size_t)M * a.K * sizeof(bf16_t) : 0;
-    hipLaunchKernelGGL((gemv_dot2_kernel<M, R, KU, XMODE, XLDS, EPI>), dim3(blocks), dim3(GEMV_THREADS),
+    Q3_LAUNCH((gemv_dot2_kernel<M, R, KU, XMODE, XLDS, EPI>), dim3(blocks), dim3(GEMV_THREADS),
                        shmem, stream, a);
     Q3_CHECK_LAUNCH();
 }

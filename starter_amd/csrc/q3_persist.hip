@@ -1329,6 +1329,6 @@ extern "C" int q3_decode_persistent(const q3_layer* layers, int L, const uint16_
     a.L = L; a.H = H; a.I = I; a.V = V; a.Hq = Hq; a.Hkv = Hkv; a.capacity = capacity;
     a.eps = eps;
     a.scale = scale;
-    hipLaunchKernelGGL(decode_persist_kernel, dim3(grid), dim3(PTHREADS), LDS_BYTES - sizeof(Smem), stream, a);
+    Q3_LAUNCH(decode_persist_kernel, dim3(grid), dim3(PTHREADS), LDS_BYTES - sizeof(Smem), stream, a);
     Q3_CHECK_LAUNCH();
 }

@@ -272,7 +272,7 @@ extern "C" int q3_rmsnorm(const bf16_t* x, int ldx, const bf16_t* w, bf16_t* y, 
     if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || ldx % 8 || ldy % 8 ||
         !aligned16(x) || !aligned16(y) || !aligned16(w))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<SRC_PLAIN>, dim3(rows), dim3(THREADS), 0, stream, x, ldx, nullptr,
+    Q3_LAUNCH(rmsnorm_kernel<SRC_PLAIN>, dim3(rows), dim3(THREADS), 0, stream, x, ldx, nullptr,
                        nullptr, nullptr, w, y, ldy, cols, eps);
     Q3_CHECK_LAUNCH();
 }
@@ -282,7 +282,7 @@ extern "C" int q3_add_rmsnorm(const bf16_t* res, const bf16_t* delta, bf16_t* su
     if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || !aligned16(res) ||
         !aligned16(delta) || !aligned16(sum_out) || !aligned16(y) || !aligned16(w))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<SRC_ADD>, dim3(rows), dim3(THREADS), 0, stream, res, cols, delta,
+    Q3_LAUNCH(rmsnorm_kernel<SRC_ADD>, dim3(rows), dim3(THREADS), 0, stream, res, cols, delta,
                        nullptr, sum_out, w, y, cols, cols, eps);
     Q3_CHECK_LAUNCH();
 }
@@ -293,13 +293,13 @@ extern "C" int q3_add_rmsnorm_partials(const float* ws, int splits, bf16_t* resi
         splits > MAX_PARTIAL_SPLITS || !ws || !aligned16(ws) || !aligned16(resid) || !aligned16(y) || !aligned16(w))
         return (int)hipErrorInvalidValue;
     if (splits <= 4)
-        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<4>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
+        Q3_LAUNCH(add_rmsnorm_partials_kernel<4>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
                            resid, w, y, cols, eps);
     else if (splits <= 8)
-        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<8>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
+        Q3_LAUNCH(add_rmsnorm_partials_kernel<8>, dim3(rows), dim3(THREADS), 0, stream, ws, splits, rows,
                            resid, w, y, cols, eps);
     else
-        hipLaunchKernelGGL(add_rmsnorm_partials_kernel<MAX_PARTIAL_SPLITS>, dim3(rows), dim3(THREADS), 0, stream, ws,
+        Q3_LAUNCH(add_rmsnorm_partials_kernel<MAX_PARTIAL_SPLITS>, dim3(rows), dim3(THREADS), 0, stream, ws,
                            splits, rows, resid, w, y, cols, eps);
     Q3_CHECK_LAUNCH();
 }
@@ -309,7 +309,7 @@ extern "C" int q3_embed_rmsnorm(const int64_t* ids, const bf16_t* embed, bf16_t*
     if (rows < 1 || cols < 8 || cols % 8 || cols > MAX_CHUNKS * THREADS * 8 || !ids || !aligned16(embed) ||
         !aligned16(resid) || !aligned16(y) || !aligned16(w))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<SRC_EMBED>, dim3(rows), dim3(THREADS), 0, stream, embed, cols, nullptr,
+    Q3_LAUNCH(rmsnorm_kernel<SRC_EMBED>, dim3(rows), dim3(THREADS), 0, stream, embed, cols, nullptr,
                        ids, resid, w, y, cols, cols, eps);
     Q3_CHECK_LAUNCH();
 }
@@ -322,7 +322,7 @@ extern "C" int q3_qk_norm_rope_kv(const bf16_t* qkv, int ld_qkv, const bf16_t* q
     if (B < 1 || T < 1 || Hq < 1 || Hkv < 1 || D != 128 || ld_qkv < (Hq + 2 * Hkv) * D || capacity < 1 ||
         start_offset < 0 || (!start_pos && start_offset + T > capacity))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(B * T), dim3(THREADS), 0, stream, qkv, ld_qkv, q_norm_w,
+    Q3_LAUNCH(qk_norm_rope_kv_kernel, dim3(B * T), dim3(THREADS), 0, stream, qkv, ld_qkv, q_norm_w,
                        k_norm_w, cos_table, sin_table, start_pos, start_offset, q_out, cache_k, cache_v, T, Hq,
                        Hkv, capacity, eps);
     Q3_CHECK_LAUNCH();
@@ -331,7 +331,7 @@ extern "C" int q3_qk_norm_rope_kv(const bf16_t* qkv, int ld_qkv, const bf16_t* q
 extern "C" int q3_argmax_finish(const float* part_val, const int* part_idx, int nparts, int B, int64_t* tokens,
                                 int64_t* pos, hipStream_t stream) {
     if (nparts < 1 || B < 1 || !part_val || !part_idx || !tokens) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(FIN_THREADS), 0, stream, part_val, part_idx, nparts,
+    Q3_LAUNCH(argmax_finish_kernel, dim3(B), dim3(FIN_THREADS), 0, stream, part_val, part_idx, nparts,
                        B, tokens, pos);
     Q3_CHECK_LAUNCH();
 }
@@ -339,6 +339,6 @@ extern "C" int q3_argmax_finish(const float* part_val, const int* part_idx, int 
 extern "C" int q3_argmax_rows(const bf16_t* logits, int ld, int B, int V, int64_t* tokens, int64_t* pos,
                               hipStream_t stream) {
     if (B < 1 || V < 1 || ld < V || !logits || !tokens) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, tokens, pos);
+    Q3_LAUNCH(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, tokens, pos);
     Q3_CHECK_LAUNCH();
 }

@@ -6,11 +6,12 @@
 // byte once, but the arithmetic (2*M flops per weight) is beyond the VALU, so
 // the weights stream straight from HBM into v_mfma_f32_16x16x32_bf16 A
 // operands:
-//   * a workgroup owns 64 weight rows (16 per wave) and one K range; the four
-//     lanes of a row read 64 contiguous bytes per load instruction, and weight
-//     loads run two 256-element chunks ahead of the MFMAs;
+//   * a workgroup owns 16 weight rows per wave (four or five waves) and one K
+//     range; the four lanes of a row read 64 contiguous bytes per load
+//     instruction, and weight loads run two or three 256-element chunks ahead
+//     of the MFMAs;
 //   * the batch rows x[0..M) for the chunk are staged once per workgroup in LDS
-//     (16-byte chunks XOR-swizzled by row) and feed all four waves as B operands;
+//     (16-byte chunks XOR-swizzled by row) and feed all its waves as B operands;
 //   * narrow matrices split K over workgroups; FP32 partials are summed in a
 //     fixed order by q3_skinny_reduce, which applies the epilogue.  With one
 //     split the epilogue runs here.
@@ -24,7 +25,6 @@
 namespace {
 
 constexpr int THREADS = 256;
-constexpr int ROWS = 64;  // weight rows per workgroup (16 per wave)
 constexpr int KC = 256;   // K elements per chunk (two 128-element sub-chunks)
 
 // x tile [16*MT rows][KC] BF16: 32 chunks of 16 bytes per row, swizzled so the
@@ -45,23 +45,28 @@ struct SkinnyArgs {
     int* part_idx;              //   and their rows (first on ties)
 };
 
-template <int MT>
-__device__ __forceinline__ void load_x(const SkinnyArgs& a, int k0, uint4 (&xr)[MT * 2]) {
-    // 16*MT rows x 32 chunks = 512*MT chunks over 256 threads.
+// x chunks per thread: 16*MT rows x 32 chunks = 512*MT chunks over NT threads
+// (rounded up; chunk indices past the tile are skipped).
+template <int MT, int NT>
+constexpr int XN = (512 * MT + NT - 1) / NT;
+
+template <int MT, int NT>
+__device__ __forceinline__ void load_x(const SkinnyArgs& a, int k0, uint4 (&xr)[XN<MT, NT>]) {
 #pragma unroll
-    for (int j = 0; j < MT * 2; ++j) {
-        const int e = threadIdx.x + j * THREADS;
+    for (int j = 0; j < XN<MT, NT>; ++j) {
+        const int e = threadIdx.x + j * NT;
         const int r = e >> 5, c = e & 31;
         xr[j] = make_uint4(0, 0, 0, 0);
         if (r < a.M) xr[j] = *reinterpret_cast<const uint4*>(a.x + (int64_t)r * a.ldx + k0 + 8 * c);
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void store_x(bf16_t* xs, const uint4 (&xr)[MT * 2]) {
+template <int MT, int NT>
+__device__ __forceinline__ void store_x(bf16_t* xs, const uint4 (&xr)[XN<MT, NT>]) {
 #pragma unroll
-    for (int j = 0; j < MT * 2; ++j) {
-        const int e = threadIdx.x + j * THREADS;
+    for (int j = 0; j < XN<MT, NT>; ++j) {
+        const int e = threadIdx.x + j * NT;
+        if ((512 * MT) % NT != 0 && e >= 512 * MT) break;
         const int r = e >> 5, c = e & 31;
         *reinterpret_cast<uint4*>(xs + r * KC + xsw(r, c) * 8) = xr[j];
     }
@@ -138,12 +143,15 @@ __device__ __forceinline__ void argmax_epilogue(const SkinnyArgs& a, const f32x4
 // register ring, x XA chunks ahead (registers, then a double-buffered LDS
 // tile).  Storing x(c+1) waits only for the loads issued before it; the later
 // weight and x loads stay in flight (vector memory counters retire in order).
-template <int MT, int NCH, bool TILED>
-__global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
+// WAVES waves of 16 weight rows share one x tile (the launch plan picks four
+// or five to spread the rows evenly over the CUs).
+template <int MT, int NCH, bool TILED, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
+    constexpr int NT = WAVES * 64;
     __shared__ __align__(16) bf16_t xs[2][16 * MT * KC];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, n = lane & 15;
-    const int row0 = blockIdx.x * ROWS + wave * 16;
+    const int row0 = blockIdx.x * (16 * WAVES) + wave * 16;
     const int split = blockIdx.y;
     const int kbeg = split * a.kper;
     const int kend = min(kbeg + a.kper, a.K);
@@ -172,21 +180,21 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
     // the registers allow the deeper prefetch; at MT >= 3 it would cost
     // occupancy.
     constexpr int WA = MT <= 2 ? 3 : 2, XA = 2;
-    uint4 w[WA + 1][8], xr[XA][MT * 2];
+    uint4 w[WA + 1][8], xr[XA][XN<MT, NT>];
 #pragma unroll
     for (int i = 0; i < XA; ++i)
-        if (kbeg + i * KC < kend) load_x<MT>(a, kbeg + i * KC, xr[i]);
+        if (kbeg + i * KC < kend) load_x<MT, NT>(a, kbeg + i * KC, xr[i]);
 #pragma unroll
     for (int i = 0; i < WA; ++i)
         if (active && kbeg + i * KC < kend) load(kbeg + i * KC, w[i]);
-    store_x<MT>(xs[0], xr[0]);
+    store_x<MT, NT>(xs[0], xr[0]);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int k0 = kbeg + c * KC;
         if (k0 < kend) {
             // x(c) is in LDS, so its register set takes x(c + XA).
-            if (k0 + XA * KC < kend) load_x<MT>(a, k0 + XA * KC, xr[c % XA]);
+            if (k0 + XA * KC < kend) load_x<MT, NT>(a, k0 + XA * KC, xr[c % XA]);
             if (active && k0 + WA * KC < kend) load(k0 + WA * KC, w[(c + WA) % (WA + 1)]);
             if (active) {
                 const bf16_t* xb = xs[c & 1];
@@ -202,13 +210,15 @@ __global__ __launch_bounds__(THREADS) void skinny_kernel(SkinnyArgs a) {
                     }
                 }
             }
-            if (k0 + KC < kend) store_x<MT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
+            if (k0 + KC < kend) store_x<MT, NT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
             __syncthreads();
         }
     }
-    if (a.epi == Q3_EPI_ARGMAX || a.epi == Q3_EPI_STORE_ARGMAX) {
-        argmax_epilogue<MT>(a, acc, row0, wave, lane, reinterpret_cast<float*>(xs));
-        return;
+    if constexpr (WAVES == 4) {
+        if (a.epi == Q3_EPI_ARGMAX || a.epi == Q3_EPI_STORE_ARGMAX) {
+            argmax_epilogue<MT>(a, acc, row0, wave, lane, reinterpret_cast<float*>(xs));
+            return;
+        }
     }
     if (!active) return;
 
@@ -272,24 +282,36 @@ __global__ __launch_bounds__(THREADS) void skinny_reduce_kernel(const float* ws,
     }
 }
 
-template <int MT, bool TILED>
+template <int MT, bool TILED, int WAVES>
 int launch_nch(int nch, dim3 grid, const SkinnyArgs& a, hipStream_t stream) {
     switch (nch) {
-#define Q3_SK(n) \
-    case n: hipLaunchKernelGGL((skinny_kernel<MT, n, TILED>), grid, dim3(THREADS), 0, stream, a); return 0;
+#define Q3_SK(n)                                                                                     \
+    case n:                                                                                          \
+        Q3_LAUNCH((skinny_kernel<MT, n, TILED, WAVES>), grid, dim3(WAVES * 64), 0, stream, a); \
+        return 0;
         Q3_SK(1) Q3_SK(2) Q3_SK(3) Q3_SK(4) Q3_SK(5) Q3_SK(6) Q3_SK(8) Q3_SK(10)
 #undef Q3_SK
     }
     return -1;
 }
 
-template <bool TILED>
+template <bool TILED, int WAVES>
 int launch_mt(int mt, int nch, dim3 grid, const SkinnyArgs& a, hipStream_t stream) {
     switch (mt) {
-        case 1: return launch_nch<1, TILED>(nch, grid, a, stream);
-        case 2: return launch_nch<2, TILED>(nch, grid, a, stream);
-        case 3: return launch_nch<3, TILED>(nch, grid, a, stream);
-        case 4: return launch_nch<4, TILED>(nch, grid, a, stream);
+        case 1: return launch_nch<1, TILED, WAVES>(nch, grid, a, stream);
+        case 2: return launch_nch<2, TILED, WAVES>(nch, grid, a, stream);
+        case 3: return launch_nch<3, TILED, WAVES>(nch, grid, a, stream);
+        case 4: return launch_nch<4, TILED, WAVES>(nch, grid, a, stream);
+    }
+    return -1;
+}
+
+// Row-major weights: four waves.  Tiled weights: four or five.
+int launch_any(bool tiled, int waves, int mt, int nch, dim3 grid, const SkinnyArgs& a, hipStream_t stream) {
+    if (!tiled) return waves == 4 ? launch_mt<false, 4>(mt, nch, grid, a, stream) : -1;
+    switch (waves) {
+        case 4: return launch_mt<true, 4>(mt, nch, grid, a, stream);
+        case 5: return launch_mt<true, 5>(mt, nch, grid, a, stream);
     }
     return -1;
 }
@@ -311,11 +333,14 @@ __global__ __launch_bounds__(THREADS) void tile16_kernel(const bf16_t* w, int N,
 // Chunks per split (compile-time in the kernel).
 constexpr int NCH_OPTIONS[] = {1, 2, 3, 4, 5, 6, 8, 10};
 
-extern "C" int q3_skinny_splits(int M, int N, int K) {
-    // More splits give more workgroups (target >= 512, two per CU) but cost
-    // FP32 partial traffic of 8*splits*M*N bytes (write + read) against the
-    // weights' 2*N*K; keep that under ~20%.  Each split keeps >= 2 chunks.
-    const int tiles = (N + ROWS - 1) / ROWS;
+namespace {
+
+// Split count of the generic plan: more splits give more workgroups (target
+// >= 512 four-wave workgroups, two per CU) but cost FP32 partial traffic of
+// 8*splits*M*N bytes (write + read) against the weights' 2*N*K; keep that
+// under ~20%.  Each split keeps >= 2 chunks.
+int generic_splits(int M, int N, int K) {
+    const int tiles = (N + 63) / 64;
     const int chunks = K / KC;
     int best = 1;
     for (int s = 2; s <= 16 && tiles * best < 512; ++s) {
@@ -343,6 +368,35 @@ extern "C" int q3_skinny_splits(int M, int N, int K) {
     return best;
 }
 
+struct Plan {
+    int waves;   // 16-row weight tiles per workgroup (one per wave)
+    int splits;  // K ranges
+};
+
+// Launch shape of a tiled projection.  A CU streams at most ~27 GB/s, so a
+// projection is fast when about 256 workgroups (one per CU) each stream an
+// equal share and the split-K partials stay few.  For the Qwen3-4B decode
+// projections the best measured shapes on MI355X (rows 16 / 32 / 64, every
+// feasible wave and split count) are:
+//   qkv     N=6144  K=2560: 4 waves x 5 splits (480 workgroups);
+//   o       N=2560  K=4096: 5 x 8 at <= 16 rows, 5 x 4 at <= 32, 4 x 4 above;
+//   gate/up N=19456 K=2560: 5 x 1 (244 workgroups, SwiGLU in the epilogue,
+//                           no partials): 22-24% faster than 4 x 2 + reduce;
+//   down    N=2560  K=9728: 4 x 7 at <= 16 rows, 5 x 8 above.
+// Other shapes take four waves and the generic split count.
+Plan skinny_plan(int M, int N, int K) {
+    const int mt = (M + 15) / 16;
+    if (N == 6144 && K == 2560) return {4, 5};
+    if (N == 2560 && K == 4096) return mt == 1 ? Plan{5, 8} : mt == 2 ? Plan{5, 4} : Plan{4, 4};
+    if (N == 19456 && K == 2560) return {5, 1};
+    if (N == 2560 && K == 9728) return mt == 1 ? Plan{4, 7} : Plan{5, 8};
+    return {4, generic_splits(M, N, K)};
+}
+
+}  // namespace
+
+extern "C" int q3_skinny_splits(int M, int N, int K) { return skinny_plan(M, N, K).splits; }
+
 extern "C" int q3_skinny_ws_floats(int M, int N, int K) {
     const int s = q3_skinny_splits(M, N, K);
     return s > 1 ? s * M * N : 0;
@@ -369,21 +423,23 @@ int skinny_launch(bool tiled, bool part_only, const bf16_t* x, int ldx, const bf
     const int chunks = K / KC;
     const int kper = (chunks + splits - 1) / splits * KC;
     SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws, part_only, part_val, part_idx};
-    const dim3 grid(N / ROWS, splits);
+    // The argmax epilogue is written for four waves; row-major weights take four.
+    const int waves = (argmax || !tiled) ? 4 : skinny_plan(M, N, K).waves;
+    const dim3 grid((N / 16 + waves - 1) / waves, splits);
     const int mt = (M + 15) / 16;
     const int nch = kper / KC;
-    const int bad = tiled ? launch_mt<true>(mt, nch, grid, a, stream) : launch_mt<false>(mt, nch, grid, a, stream);
+    const int bad = launch_any(tiled, waves, mt, nch, grid, a, stream);
     if (bad) return (int)hipErrorInvalidValue;
     hipError_t rc = hipGetLastError();
     if (rc != hipSuccess || splits == 1 || part_only) return (int)rc;
     const int64_t pairs = (int64_t)M * (N / 2);
     const dim3 rgrid((unsigned)((pairs + THREADS - 1) / THREADS));
     if (splits <= 4)
-        hipLaunchKernelGGL(skinny_reduce_kernel<4>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
+        Q3_LAUNCH(skinny_reduce_kernel<4>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
     else if (splits <= 8)
-        hipLaunchKernelGGL(skinny_reduce_kernel<8>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
+        Q3_LAUNCH(skinny_reduce_kernel<8>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi, y, ldy);
     else
-        hipLaunchKernelGGL(skinny_reduce_kernel<MAX_SPLITS>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi,
+        Q3_LAUNCH(skinny_reduce_kernel<MAX_SPLITS>, rgrid, dim3(THREADS), 0, stream, ws, splits, M, N, epi,
                            y, ldy);
     Q3_CHECK_LAUNCH();
 }
@@ -418,7 +474,7 @@ extern "C" int q3_tile16(const bf16_t* w, int N, int K, bf16_t* out, hipStream_t
         ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15))
         return (int)hipErrorInvalidValue;
     const int64_t pieces = (int64_t)N / 16 * (K / 32) * 64;
-    hipLaunchKernelGGL(tile16_kernel, dim3((unsigned)((pieces + THREADS - 1) / THREADS)), dim3(THREADS), 0, stream, w,
+    Q3_LAUNCH(tile16_kernel, dim3((unsigned)((pieces + THREADS - 1) / THREADS)), dim3(THREADS), 0, stream, w,
                        N, K, out);
     Q3_CHECK_LAUNCH();
 }
