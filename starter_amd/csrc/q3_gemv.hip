@@ -32,7 +32,7 @@
 
 namespace {
 
-constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_THREADS = 256;  // four waves; plain-input launches may take five
 constexpr int GEMV_WAVES = GEMV_THREADS / Q3_WAVE;
 constexpr int LDS_X_LIMIT = 60 * 1024;
 
@@ -58,14 +58,15 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-// Stage the M input rows into LDS (BF16), normalised for the NORM modes.
-template <int M, int XMODE>
+// Stage the M input rows into LDS (BF16), normalised for the NORM modes
+// (W waves per workgroup; the NORM modes are written for four).
+template <int M, int XMODE, int W>
 __device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int chunks = a.K >> 3;
     if constexpr (XMODE == Q3_X_PLAIN) {
-        for (int c = tid; c < chunks; c += GEMV_THREADS)
+        for (int c = tid; c < chunks; c += W * Q3_WAVE)
 #pragma unroll
             for (int m = 0; m < M; ++m)
                 *reinterpret_cast<uint4*>(xs + m * a.K + c * 8) =
@@ -73,6 +74,7 @@ __device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
         __syncthreads();
         return;
     } else {
+        static_assert(W == GEMV_WAVES, "the norm prologue is written for four waves");
         // One round trip: the rows and the gain are loaded together and kept in
         // registers (K <= 4096: at most two chunks per thread), squared and
         // summed, block-reduced, then normalised straight into LDS.
@@ -263,12 +265,15 @@ __device__ void argmax_epilogue(const GemvArgs& a, const float (&acc)[R][M], int
 }
 
 // KU > 0: K == 512*KU, all weight loads issued up front.  KU == 0: any K % 8 == 0.
-template <int M, int R, int KU, int XMODE, bool XLDS, int EPI>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
+// W waves per workgroup (four, or five for plain inputs).
+template <int M, int R, int KU, int XMODE, bool XLDS, int EPI, int W>
+__global__ __launch_bounds__(W * Q3_WAVE) void gemv_dot2_kernel(GemvArgs a) {
+    static_assert(W == GEMV_WAVES || (EPI != Q3_EPI_ARGMAX && EPI != Q3_EPI_STORE_ARGMAX),
+                  "the argmax epilogue is written for four waves");
     extern __shared__ __align__(16) unsigned char smem[];
     bf16_t* xs = reinterpret_cast<bf16_t*>(smem);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+    const int row0 = (blockIdx.x * W + wave) * R;
     const bool active = row0 < a.N;
     const int K = a.K;
     const bf16_t* wrow = a.w + (int64_t)row0 * K + lane * 8;
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) wv[r][u] = load_nt(wrow + (int64_t)r * K + u * 512);
         }
-        if constexpr (XLDS) stage_x<M, XMODE>(a, xs);
+        if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
         if (active) {
 #pragma unroll
             for (int u = 0; u < KU; ++u)
@@ -299,7 +304,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_dot2_kernel(GemvArgs a) {
                 }
         }
     } else {
-        if constexpr (XLDS) stage_x<M, XMODE>(a, xs);
+        if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
         if (active) {
             for (int k = lane * 8; k < K; k += 512) {
                 uint4 wv[R];
@@ -347,15 +352,35 @@ constexpr bool combo_used(int xmode, int epi) {
          : true;
 }
 
-template <int M, int KU, int XMODE, bool XLDS, int EPI>
-int launch_one(const GemvArgs& a, hipStream_t stream) {
+// Waves per workgroup.  A CU streams at most ~27 GB/s, so a launch is as slow
+// as its most loaded CU: plain-input projections take five waves when that
+// spreads the rows more evenly over the 256 CUs (N = 2560: 512 workgroups,
+// two per CU, against 640 = 2.5 per CU with four).
+int waves_for(int xmode, int epi, int M, int N) {
+    constexpr int CUS = 256;
+    if (xmode != Q3_X_PLAIN || epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) return GEMV_WAVES;
+    const int units = N / rows_per_wave(M, epi);
+    auto load = [&](int w) { return ((units + w - 1) / w + CUS - 1) / CUS * w; };
+    return load(5) < load(GEMV_WAVES) ? 5 : GEMV_WAVES;
+}
+
+template <int M, int KU, int XMODE, bool XLDS, int EPI, int W>
+int launch_w(const GemvArgs& a, hipStream_t stream) {
     constexpr int R = rows_per_wave(M, EPI);
     if (a.N % R != 0) return -1;
-    const int blocks = (a.N / R + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int blocks = (a.N / R + W - 1) / W;
     const size_t shmem = XLDS ? (size_t)M * a.K * sizeof(bf16_t) : 0;
-    Q3_LAUNCH((gemv_dot2_kernel<M, R, KU, XMODE, XLDS, EPI>), dim3(blocks), dim3(GEMV_THREADS),
-                       shmem, stream, a);
+    Q3_LAUNCH((gemv_dot2_kernel<M, R, KU, XMODE, XLDS, EPI, W>), dim3(blocks), dim3(W * Q3_WAVE), shmem, stream,
+              a);
     Q3_CHECK_LAUNCH();
+}
+
+template <int M, int KU, int XMODE, bool XLDS, int EPI>
+int launch_one(const GemvArgs& a, hipStream_t stream) {
+    if constexpr (XMODE == Q3_X_PLAIN && EPI != Q3_EPI_ARGMAX && EPI != Q3_EPI_STORE_ARGMAX) {
+        if (waves_for(XMODE, EPI, M, a.N) == 5) return launch_w<M, KU, XMODE, XLDS, EPI, 5>(a, stream);
+    }
+    return launch_w<M, KU, XMODE, XLDS, EPI, GEMV_WAVES>(a, stream);
 }
 
 template <int M, int XMODE, bool XLDS, int EPI>
