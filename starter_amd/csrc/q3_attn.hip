@@ -165,7 +165,8 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 }
 
 // grid (splits, Hkv, B), WAVES waves per workgroup; wave w takes blocks w,
-// w+WAVES, ... of the split's key range with two register sets in flight (the
+// w+WAVES, ... of the split's key range (or, with several splits, the w-th
+// contiguous quarter of it) with two register sets in flight (the
 // loop is unrolled by two so neither set is ever copied: a copy would wait for
 // the newest loads, as vector memory counters retire in order); the waves
 // merge through LDS; attn_merge_kernel merges the splits, or with one split the
@@ -196,7 +197,13 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
     float q_lo = 0.f, q_hi = 0.f;
     if (w < GROUP) qkv_pair(a, b, (kvh * GROUP + w) * D + lane, q_lo, q_hi);
     KVRegs ra, rb;
-    const int first = begin + w * BLK;
+    // Split ranges are always whole (only the last live split is partial), so
+    // with several splits each wave streams one contiguous quarter of its
+    // split (fewer concurrent streams: 5% faster at 16K context); one split may
+    // be far from full (512 of 768 keys), so its waves interleave blocks.
+    const bool contig = a.splits > 1;
+    const int wq = split_len(range_end - begin, WAVES);
+    const int first = contig ? begin + w * wq : begin + w * BLK;
     if (first < range_end) load_kv(ra, kbase, vbase, first, range_end - 1, lane);
 
     const bool bad_pos = pos_raw < 0 || pos_raw >= a.capacity;
@@ -255,8 +262,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
             if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * kk + 8 * g]);
             st.qb[kk] = as_bf16x8(v);
         }
-        const int stride = WAVES * BLK;
-        const int nblk = (end - first + stride - 1) / stride;
+        const int stride = contig ? BLK : WAVES * BLK;
+        const int wend = contig ? min(first + wq, end) : end;
+        const int nblk = (wend - first + stride - 1) / stride;
         auto sub = [&](int blk) { return (owner && blk <= pos && pos < blk + BLK) ? pos - blk : -1; };
         // Every load inside the loop is unconditional and the last one or two
         // blocks are peeled: the compiler's wait counting, which merges
@@ -488,14 +496,13 @@ __global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, 
 extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     // One split (no merge launch: the kernel writes the output) once there are
     // enough (sequence, KV head) pairs to occupy half the CUs at moderate
-    // context, or every CU twice at any context.  Otherwise about 1024
-    // workgroups (two resident per CU, two rounds) with at least 256 keys (two
-    // blocks per wave) per split; when even that leaves CUs idle (short
-    // contexts at small batch), 128 keys per split to spread the latency-bound
-    // work.
+    // context, or every CU twice at any context.  Otherwise about 512
+    // workgroups (two resident per CU) with at least 256 keys (two blocks per
+    // wave) per split; when even that leaves CUs idle (short contexts at small
+    // batch), 128 keys per split to spread the latency-bound work.
     const long heads = (long)B * Hkv;
     if (heads >= 512 || (heads >= 128 && capacity <= 4096)) return 1;
-    const long want = (1024 + heads - 1) / heads;
+    const long want = (512 + heads - 1) / heads;
     long most = (capacity + 255) / 256;
     if (heads * most < 128) most = (capacity + 127) / 128;
     const long s = want < most ? want : most;
