@@ -149,6 +149,103 @@ __device__ void stage_x(const GemvArgs& a, bf16_t* xs) {
     }
 }
 
+// The same staging in two halves for K = 512*KU: the input rows (and gain)
+// are loaded into registers before the weight loads are issued, so waiting
+// for them does not wait for the weights (vector memory counters retire in
+// order), and the norm / copy runs while the weights are still in flight.
+// Arithmetic and order are those of stage_x.
+template <int XMODE, int KU, int W>
+constexpr int x_chunks() {
+    return (64 * KU + W * Q3_WAVE - 1) / (W * Q3_WAVE);
+}
+
+template <int M, int XMODE, int KU, int W>
+__device__ __forceinline__ void stage_x_issue(const GemvArgs& a, u32x4_t (&xv)[x_chunks<XMODE, KU, W>()][M],
+                                              u32x4_t (&gv)[x_chunks<XMODE, KU, W>()]) {
+    constexpr int XC = x_chunks<XMODE, KU, W>();
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = tid + j * W * Q3_WAVE;
+        if (c < 64 * KU) {
+            if constexpr (XMODE == Q3_X_NORM) gv[j] = *reinterpret_cast<const u32x4_t*>(a.norm_w + c * 8);
+#pragma unroll
+            for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + c * 8);
+        }
+    }
+}
+
+template <int M, int XMODE, int KU, int W>
+__device__ __forceinline__ void stage_x_finish(const GemvArgs& a, const u32x4_t (&xv)[x_chunks<XMODE, KU, W>()][M],
+                                               const u32x4_t (&gv)[x_chunks<XMODE, KU, W>()], bf16_t* xs) {
+    constexpr int XC = x_chunks<XMODE, KU, W>();
+    constexpr int K = 512 * KU;
+    const int tid = threadIdx.x;
+    if constexpr (XMODE == Q3_X_PLAIN) {
+#pragma unroll
+        for (int j = 0; j < XC; ++j) {
+            const int c = tid + j * W * Q3_WAVE;
+            if (c < 64 * KU)
+#pragma unroll
+                for (int m = 0; m < M; ++m) *reinterpret_cast<u32x4_t*>(xs + m * K + c * 8) = xv[j][m];
+        }
+        __syncthreads();
+    } else {
+        static_assert(XMODE == Q3_X_NORM && W == GEMV_WAVES, "norm staging is written for four waves");
+        const int lane = tid & 63, wave = tid >> 6;
+        __shared__ float red[GEMV_WAVES][M];
+        float ss[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) ss[m] = 0.f;
+#pragma unroll
+        for (int j = 0; j < XC; ++j) {
+            const int c = tid + j * W * Q3_WAVE;
+            if (c < 64 * KU) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const u32x4_t v = xv[j][m];
+                    float s = ss[m];
+                    s += bflo(v.x) * bflo(v.x); s += bfhi(v.x) * bfhi(v.x);
+                    s += bflo(v.y) * bflo(v.y); s += bfhi(v.y) * bfhi(v.y);
+                    s += bflo(v.z) * bflo(v.z); s += bfhi(v.z) * bfhi(v.z);
+                    s += bflo(v.w) * bflo(v.w); s += bfhi(v.w) * bfhi(v.w);
+                    ss[m] = s;
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = wave_sum(ss[m]);
+            if (lane == 0) red[wave][m] = s;
+        }
+        __syncthreads();
+        float inv[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+            inv[m] = inv_rms(s, K, a.eps);
+        }
+#pragma unroll
+        for (int j = 0; j < XC; ++j) {
+            const int c = tid + j * W * Q3_WAVE;
+            if (c < 64 * KU) {
+                const u32x4_t g = gv[j];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    u32x4_t v = xv[j][m];
+                    const float im = inv[m];
+                    v.x = pack2(norm_elem(bflo(v.x), im, bflo(g.x)), norm_elem(bfhi(v.x), im, bfhi(g.x)));
+                    v.y = pack2(norm_elem(bflo(v.y), im, bflo(g.y)), norm_elem(bfhi(v.y), im, bfhi(g.y)));
+                    v.z = pack2(norm_elem(bflo(v.z), im, bflo(g.z)), norm_elem(bfhi(v.z), im, bfhi(g.z)));
+                    v.w = pack2(norm_elem(bflo(v.w), im, bflo(g.w)), norm_elem(bfhi(v.w), im, bfhi(g.w)));
+                    *reinterpret_cast<u32x4_t*>(xs + m * K + c * 8) = v;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // x chunk (16 bytes) of batch row m at element k, from LDS or global.
 template <bool XLDS>
 __device__ __forceinline__ uint4 xchunk(const GemvArgs& a, const bf16_t* xs, int m, int k) {
@@ -285,6 +382,11 @@ __global__ __launch_bounds__(W * Q3_WAVE) void gemv_dot2_kernel(GemvArgs a) {
         for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
 
     if constexpr (KU > 0) {
+        // Input rows first unless they come from the embedding (ids first).
+        constexpr bool SPLIT = XLDS && XMODE != Q3_X_EMBED_NORM;
+        constexpr int XC = x_chunks<XMODE, KU, W>();
+        u32x4_t xv[XC][M], gv[XC];
+        if constexpr (SPLIT) stage_x_issue<M, XMODE, KU, W>(a, xv, gv);
         uint4 wv[R][KU];
         if (active) {
 #pragma unroll
@@ -292,7 +394,8 @@ __global__ __launch_bounds__(W * Q3_WAVE) void gemv_dot2_kernel(GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) wv[r][u] = load_nt(wrow + (int64_t)r * K + u * 512);
         }
-        if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
+        if constexpr (SPLIT) stage_x_finish<M, XMODE, KU, W>(a, xv, gv, xs);
+        else if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
         if (active) {
 #pragma unroll
             for (int u = 0; u < KU; ++u)
@@ -388,7 +491,9 @@ int launch_ku(const GemvArgs& a, hipStream_t stream) {
     switch (a.K) {
         case 2560: return launch_one<M, 5, XMODE, XLDS, EPI>(a, stream);
         case 4096: return launch_one<M, 8, XMODE, XLDS, EPI>(a, stream);
-        case 9728: return launch_one<M, 19, XMODE, XLDS, EPI>(a, stream);
+        case 9728:  // above Q3_GEMV_MAX_NORM_K: plain input only
+            if constexpr (XMODE == Q3_X_PLAIN) return launch_one<M, 19, XMODE, XLDS, EPI>(a, stream);
+            return -1;
     }
     return launch_one<M, 0, XMODE, XLDS, EPI>(a, stream);
 }
