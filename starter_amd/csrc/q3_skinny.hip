@@ -72,6 +72,32 @@ __device__ __forceinline__ void store_x(bf16_t* xs, const uint4 (&xr)[XN<MT, NT>
     }
 }
 
+// Branch-free variants for splits whose every chunk is in range: rows past M
+// re-read row M-1 and chunk indices past the tile re-take the last chunk (the
+// duplicate stores write the same bytes to the same place), so no load sits
+// under a condition.  A load under a condition makes the compiler's wait
+// counting merge control-flow paths conservatively, and each MFMA then waits
+// for the newest loads in flight instead of its own chunk's.
+template <int MT, int NT>
+__device__ __forceinline__ void load_x_all(const SkinnyArgs& a, int k0, uint4 (&xr)[XN<MT, NT>]) {
+#pragma unroll
+    for (int j = 0; j < XN<MT, NT>; ++j) {
+        const int e = min((int)threadIdx.x + j * NT, 512 * MT - 1);
+        const int r = min(e >> 5, a.M - 1), c = e & 31;
+        xr[j] = *reinterpret_cast<const uint4*>(a.x + (int64_t)r * a.ldx + k0 + 8 * c);
+    }
+}
+
+template <int MT, int NT>
+__device__ __forceinline__ void store_x_all(bf16_t* xs, const uint4 (&xr)[XN<MT, NT>]) {
+#pragma unroll
+    for (int j = 0; j < XN<MT, NT>; ++j) {
+        const int e = min((int)threadIdx.x + j * NT, 512 * MT - 1);
+        const int r = e >> 5, c = e & 31;
+        *reinterpret_cast<uint4*>(xs + r * KC + xsw(r, c) * 8) = xr[j];
+    }
+}
+
 // Weight chunk of this lane: row (row0 + n), 16-byte pieces at elements
 // k0 + 32j + 8g (j = 0..7), so each load instruction covers 64 contiguous
 // bytes of each of the wave's 16 rows.
@@ -181,41 +207,70 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkinnyArgs a) {
     // occupancy.
     constexpr int WA = MT <= 2 ? 3 : 2, XA = 2;
     uint4 w[WA + 1][8], xr[XA][XN<MT, NT>];
+    // One MFMA step of chunk c from the x tile in LDS.
+    auto mfma_chunk = [&](int c) {
+        const bf16_t* xb = xs[c & 1];
 #pragma unroll
-    for (int i = 0; i < XA; ++i)
-        if (kbeg + i * KC < kend) load_x<MT, NT>(a, kbeg + i * KC, xr[i]);
+        for (int j = 0; j < 8; ++j) {
+            const bf16x8_t av = as_bf16x8(w[c % (WA + 1)][j]);
+            const int ch = 4 * j + g;  // 16-byte chunk of the x row
 #pragma unroll
-    for (int i = 0; i < WA; ++i)
-        if (active && kbeg + i * KC < kend) load(kbeg + i * KC, w[i]);
-    store_x<MT, NT>(xs[0], xr[0]);
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int k0 = kbeg + c * KC;
-        if (k0 < kend) {
-            // x(c) is in LDS, so its register set takes x(c + XA).
-            if (k0 + XA * KC < kend) load_x<MT, NT>(a, k0 + XA * KC, xr[c % XA]);
-            if (active && k0 + WA * KC < kend) load(k0 + WA * KC, w[(c + WA) % (WA + 1)]);
-            if (active) {
-                const bf16_t* xb = xs[c & 1];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const bf16x8_t av = as_bf16x8(w[c % (WA + 1)][j]);
-                    const int ch = 4 * j + g;  // 16-byte chunk of the x row
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        const int r = 16 * t + n;
-                        const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const uint4*>(xb + r * KC + xsw(r, ch) * 8));
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
-                    }
-                }
+            for (int t = 0; t < MT; ++t) {
+                const int r = 16 * t + n;
+                const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const uint4*>(xb + r * KC + xsw(r, ch) * 8));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
             }
-            if (k0 + KC < kend) store_x<MT, NT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
-            __syncthreads();
+        }
+    };
+    if (kend - kbeg == NCH * KC) {
+        // Every chunk in range (all splits but a ragged last one): no load is
+        // conditional, inactive waves compute on clamped rows and store nothing.
+#pragma unroll
+        for (int i = 0; i < XA && i < NCH; ++i) load_x_all<MT, NT>(a, kbeg + i * KC, xr[i]);
+#pragma unroll
+        for (int i = 0; i < WA && i < NCH; ++i) load(kbeg + i * KC, w[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        store_x_all<MT, NT>(xs[0], xr[0]);
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int k0 = kbeg + c * KC;
+            if (c + XA < NCH) load_x_all<MT, NT>(a, k0 + XA * KC, xr[c % XA]);
+            if (c + WA < NCH) load(k0 + WA * KC, w[(c + WA) % (WA + 1)]);
+            // Keep the prefetch here: the scheduler would otherwise sink each
+            // load down to its use and the MFMAs would wait for fresh loads.
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_chunk(c);
+            if (c + 1 < NCH) {
+                store_x_all<MT, NT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
+                __syncthreads();
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < XA; ++i)
+            if (kbeg + i * KC < kend) load_x<MT, NT>(a, kbeg + i * KC, xr[i]);
+#pragma unroll
+        for (int i = 0; i < WA; ++i)
+            if (active && kbeg + i * KC < kend) load(kbeg + i * KC, w[i]);
+        store_x<MT, NT>(xs[0], xr[0]);
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int k0 = kbeg + c * KC;
+            if (k0 < kend) {
+                // x(c) is in LDS, so its register set takes x(c + XA).
+                if (k0 + XA * KC < kend) load_x<MT, NT>(a, k0 + XA * KC, xr[c % XA]);
+                if (active && k0 + WA * KC < kend) load(k0 + WA * KC, w[(c + WA) % (WA + 1)]);
+                if (active) mfma_chunk(c);
+                if (k0 + KC < kend) store_x<MT, NT>(xs[(c + 1) & 1], xr[(c + 1) % XA]);
+                __syncthreads();
+            }
         }
     }
     if constexpr (WAVES == 4) {
         if (a.epi == Q3_EPI_ARGMAX || a.epi == Q3_EPI_STORE_ARGMAX) {
+            __syncthreads();  // the epilogue reuses the x tile, which other waves may still read
             argmax_epilogue<MT>(a, acc, row0, wave, lane, reinterpret_cast<float*>(xs));
             return;
         }
