@@ -166,12 +166,10 @@ __device__ __forceinline__ void stage_x_issue(const GemvArgs& a, u32x4_t (&xv)[x
     const int tid = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
-        const int c = tid + j * W * Q3_WAVE;
-        if (c < 64 * KU) {
-            if constexpr (XMODE == Q3_X_NORM) gv[j] = *reinterpret_cast<const u32x4_t*>(a.norm_w + c * 8);
+        const int c = min(tid + j * W * Q3_WAVE, 64 * KU - 1);  // past the row: a duplicate, never used
+        if constexpr (XMODE == Q3_X_NORM) gv[j] = *reinterpret_cast<const u32x4_t*>(a.norm_w + c * 8);
 #pragma unroll
-            for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + c * 8);
-        }
+        for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + c * 8);
     }
 }
 
@@ -387,25 +385,28 @@ __global__ __launch_bounds__(W * Q3_WAVE) void gemv_dot2_kernel(GemvArgs a) {
         constexpr int XC = x_chunks<XMODE, KU, W>();
         u32x4_t xv[XC][M], gv[XC];
         if constexpr (SPLIT) stage_x_issue<M, XMODE, KU, W>(a, xv, gv);
+        __builtin_amdgcn_sched_barrier(0);  // keep the input loads ahead of the weight loads
+        // No load under a condition (a wave past the last row re-reads the
+        // last rows and stores nothing): a conditional load makes the
+        // compiler's wait counting merge control-flow paths conservatively,
+        // and the prologue would then wait for every weight load.
+        const bf16_t* wsafe = a.w + (int64_t)min(row0, a.N - R) * K + lane * 8;
         uint4 wv[R][KU];
-        if (active) {
 #pragma unroll
-            for (int u = 0; u < KU; ++u)
+        for (int u = 0; u < KU; ++u)
 #pragma unroll
-                for (int r = 0; r < R; ++r) wv[r][u] = load_nt(wrow + (int64_t)r * K + u * 512);
-        }
+            for (int r = 0; r < R; ++r) wv[r][u] = load_nt(wsafe + (int64_t)r * K + u * 512);
+        __builtin_amdgcn_sched_barrier(0);  // and every weight load issued before the prologue
         if constexpr (SPLIT) stage_x_finish<M, XMODE, KU, W>(a, xv, gv, xs);
         else if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
-        if (active) {
 #pragma unroll
-            for (int u = 0; u < KU; ++u)
+        for (int u = 0; u < KU; ++u)
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const uint4 xv = xchunk<XLDS>(a, xs, m, lane * 8 + u * 512);
+            for (int m = 0; m < M; ++m) {
+                const uint4 xv = xchunk<XLDS>(a, xs, m, lane * 8 + u * 512);
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv[r][u], xv, acc[r][m]);
-                }
-        }
+                for (int r = 0; r < R; ++r) acc[r][m] = dot8(wv[r][u], xv, acc[r][m]);
+            }
     } else {
         if constexpr (XLDS) stage_x<M, XMODE, W>(a, xs);
         if (active) {
