@@ -434,17 +434,17 @@ struct Plan {
 // projections the best measured shapes on MI355X (rows 16 / 32 / 64, every
 // feasible wave and split count) are:
 //   qkv     N=6144  K=2560: 4 waves x 5 splits (480 workgroups);
-//   o       N=2560  K=4096: 5 x 8 at <= 16 rows, 5 x 4 at <= 32, 4 x 4 above;
+//   o       N=2560  K=4096: 5 x 8 at <= 16 rows, 4 x 6 at <= 32, 4 x 4 above;
 //   gate/up N=19456 K=2560: 5 x 1 (244 workgroups, SwiGLU in the epilogue,
 //                           no partials): 22-24% faster than 4 x 2 + reduce;
-//   down    N=2560  K=9728: 4 x 7 at <= 16 rows, 5 x 8 above.
+//   down    N=2560  K=9728: 5 x 8.
 // Other shapes take four waves and the generic split count.
 Plan skinny_plan(int M, int N, int K) {
     const int mt = (M + 15) / 16;
     if (N == 6144 && K == 2560) return {4, 5};
-    if (N == 2560 && K == 4096) return mt == 1 ? Plan{5, 8} : mt == 2 ? Plan{5, 4} : Plan{4, 4};
+    if (N == 2560 && K == 4096) return mt == 1 ? Plan{5, 8} : mt == 2 ? Plan{4, 6} : Plan{4, 4};
     if (N == 19456 && K == 2560) return {5, 1};
-    if (N == 2560 && K == 9728) return mt == 1 ? Plan{4, 7} : Plan{5, 8};
+    if (N == 2560 && K == 9728) return {5, 8};
     return {4, generic_splits(M, N, K)};
 }
 
