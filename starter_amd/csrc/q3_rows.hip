@@ -107,6 +107,54 @@ __global__ __launch_bounds__(THREADS) void add_rmsnorm_partials_kernel(const flo
     bf16_t* rrow = resid + (int64_t)row * cols;
     uint4 xv[PARTIAL_CHUNKS];
     float ss = 0.f;
+    if constexpr (MAXS <= 8) {
+        // Every load first (chunk indices past the row re-read the last chunk
+        // and are never stored), so the whole row is one memory round trip.
+        f32x4_t lo[PARTIAL_CHUNKS][MAXS], hi[PARTIAL_CHUNKS][MAXS];
+        uint4 rv[PARTIAL_CHUNKS], gv[PARTIAL_CHUNKS];
+#pragma unroll
+        for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
+            const int c = min((int)threadIdx.x + j * THREADS, chunks - 1);
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s) {
+                const float* src = ws + ((int64_t)min(s, splits - 1) * rows + row) * cols + c * 8;
+                lo[j][s] = *reinterpret_cast<const f32x4_t*>(src);
+                hi[j][s] = *reinterpret_cast<const f32x4_t*>(src + 4);
+            }
+            rv[j] = *reinterpret_cast<const uint4*>(rrow + c * 8);
+            gv[j] = *reinterpret_cast<const uint4*>(w + c * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
+            const int c = threadIdx.x + j * THREADS;
+            f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s)
+                if (s < splits) {
+                    a += lo[j][s];
+                    b += hi[j][s];
+                }
+            const uint4 r = rv[j];
+            uint4 v;
+            v.x = pack2(f2bf(bflo(r.x) + rbf(a[0])), f2bf(bfhi(r.x) + rbf(a[1])));
+            v.y = pack2(f2bf(bflo(r.y) + rbf(a[2])), f2bf(bfhi(r.y) + rbf(a[3])));
+            v.z = pack2(f2bf(bflo(r.z) + rbf(b[0])), f2bf(bfhi(r.z) + rbf(b[1])));
+            v.w = pack2(f2bf(bflo(r.w) + rbf(b[2])), f2bf(bfhi(r.w) + rbf(b[3])));
+            xv[j] = v;
+            if (c < chunks) {
+                *reinterpret_cast<uint4*>(rrow + c * 8) = v;
+                ss += sumsq8(v);
+            }
+        }
+        const float inv = inv_rms(block_sum(ss, red), cols, eps);
+#pragma unroll
+        for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
+            const int c = threadIdx.x + j * THREADS;
+            if (c < chunks) *reinterpret_cast<uint4*>(y + (int64_t)row * cols + c * 8) = norm8(xv[j], gv[j], inv);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < PARTIAL_CHUNKS; ++j) {
         const int c = threadIdx.x + j * THREADS;
