@@ -54,16 +54,20 @@ __device__ __forceinline__ bf16x8_t vt_operand(const bf16_t* vs, int dm, int n, 
 
 // Per-head RMSNorm + RoPE of one 128-wide row held as (lo = x[l], hi = x[l+64])
 // in lane l (reference fused.py:161-219): returns bf16 bits of both halves.
-__device__ __forceinline__ void norm_rope_pair(float lo, float hi, const bf16_t* w,
-                                               const bf16_t* cosr, const bf16_t* sinr,
-                                               float eps, int lane, uint32_t& out_lo,
-                                               uint32_t& out_hi) {
+// The four BF16 values a lane needs from a 128-wide row: x[lane], x[lane + 64].
+struct Pair16 {
+    bf16_t lo, hi;
+};
+__device__ __forceinline__ Pair16 pair16(const bf16_t* row, int lane) { return {row[lane], row[lane + 64]}; }
+
+__device__ __forceinline__ void norm_rope_pair(float lo, float hi, Pair16 w, Pair16 c, Pair16 sn, float eps,
+                                               uint32_t& out_lo, uint32_t& out_hi) {
     const float ss = wave_sum(lo * lo + hi * hi);
     const float inv = inv_rms(ss, D, eps);
-    const float n_lo = bf2f(norm_elem(lo, inv, bf2f(w[lane])));
-    const float n_hi = bf2f(norm_elem(hi, inv, bf2f(w[lane + 64])));
-    const float c_lo = bf2f(cosr[lane]), s_lo = bf2f(sinr[lane]);
-    const float c_hi = bf2f(cosr[lane + 64]), s_hi = bf2f(sinr[lane + 64]);
+    const float n_lo = bf2f(norm_elem(lo, inv, bf2f(w.lo)));
+    const float n_hi = bf2f(norm_elem(hi, inv, bf2f(w.hi)));
+    const float c_lo = bf2f(c.lo), s_lo = bf2f(sn.lo);
+    const float c_hi = bf2f(c.hi), s_hi = bf2f(sn.hi);
     out_lo = f2bf(rbf(n_lo * c_lo) + rbf(-n_hi * s_lo));
     out_hi = f2bf(rbf(n_hi * c_hi) + rbf(n_lo * s_hi));
 }
@@ -89,32 +93,59 @@ struct DecodeArgs {
 
 // Elements idx and idx + 64 of sequence b's projected q|k|v row: BF16 from
 // qkv, or the split partials summed in split order and rounded to BF16 (the
-// value the projection's own STORE epilogue would have written).  Splits are
-// read four at a time with every load of a group issued before the sums.
-__device__ __forceinline__ void qkv_pair(const DecodeArgs& a, int b, int idx, float& lo, float& hi) {
-    if (a.qkv_part == nullptr) {
-        const bf16_t* r = a.qkv + (int64_t)b * a.ld_qkv + idx;
-        lo = bf2f(r[0]);
-        hi = bf2f(r[64]);
+// value the projection's own STORE epilogue would have written).  The loads
+// are issued by qkv_issue and summed by qkv_finish, so a kernel can put every
+// independent load in flight before it waits for any (vector memory counters
+// retire in order).  Up to QKV_FAST splits load at once; more take a loop.
+constexpr int QKV_FAST = 8;
+// QP: 0 = BF16 row, 1 = up to QKV_FAST split partials, 2 = more partials (loop).
+template <int QP>
+struct QkvRaw {
+    bf16_t blo, bhi;  // BF16 row (converted only when used, so no wait here)
+    float lo[QP == 1 ? QKV_FAST : 1], hi[QP == 1 ? QKV_FAST : 1];
+};
+
+template <int QP>
+__device__ __forceinline__ void qkv_issue(const DecodeArgs& a, int b, int idx, QkvRaw<QP>& r) {
+    if constexpr (QP == 0) {
+        const bf16_t* row = a.qkv + (int64_t)b * a.ld_qkv + idx;
+        r.blo = row[0];
+        r.bhi = row[64];
+    } else if constexpr (QP == 1) {
+        const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;  // one split: [B, ld_qkv]
+        const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
+#pragma unroll
+        for (int j = 0; j < QKV_FAST; ++j) {
+            const int64_t o = (int64_t)min(j, a.qkv_splits - 1) * stride;
+            r.lo[j] = base[o];
+            r.hi[j] = base[o + 64];
+        }
+    }
+}
+
+template <int QP>
+__device__ __forceinline__ void qkv_finish(const DecodeArgs& a, int b, int idx, const QkvRaw<QP>& r, float& lo,
+                                           float& hi) {
+    if constexpr (QP == 0) {
+        lo = bf2f(r.blo);
+        hi = bf2f(r.bhi);
         return;
     }
-    const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;  // one split: [B, ld_qkv]
-    const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
     float slo = 0.f, shi = 0.f;
-    for (int s0 = 0; s0 < a.qkv_splits; s0 += 4) {
-        float l4[4], h4[4];
+    if constexpr (QP == 1) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t o = (int64_t)min(s0 + j, a.qkv_splits - 1) * stride;
-            l4[j] = base[o];
-            h4[j] = base[o + 64];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (s0 + j < a.qkv_splits) {
-                slo += l4[j];
-                shi += h4[j];
+        for (int j = 0; j < QKV_FAST; ++j)
+            if (j < a.qkv_splits) {
+                slo += r.lo[j];
+                shi += r.hi[j];
             }
+    } else {
+        const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;
+        const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
+        for (int s0 = 0; s0 < a.qkv_splits; ++s0) {
+            slo += base[(int64_t)s0 * stride];
+            shi += base[(int64_t)s0 * stride + 64];
+        }
     }
     lo = rbf(slo);
     hi = rbf(shi);
@@ -173,7 +204,7 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // normalised output is written here.  Eight waves (one workgroup per CU, 128 KB
 // of tiles) when the grid leaves CUs idle and every wave still gets a block:
 // twice the loads in flight per (sequence, KV head).
-template <int WAVES>
+template <int WAVES, int QP>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(DecodeArgs a) {
     static_assert(WAVES == 4 || WAVES == 8, "four or eight waves");
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -192,10 +223,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
     const bf16_t* kbase = a.cache_k + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
     const bf16_t* vbase = a.cache_v + ((int64_t)b * a.Hkv + kvh) * a.capacity * D;
 
-    // Everything that does not depend on the position is requested first.
+    // Every load that does not wait for another is issued before the first
+    // wait: the first key block, this wave's q pair, the new token's k and v
+    // pairs, the norm gains; then the RoPE rows once the (scalar) position
+    // is in.  Loads are unconditional (indices clamped), so the compiler's
+    // wait counting does not merge branches and wait for all of them.
     const int pos_raw = (int)*a.pos;
-    float q_lo = 0.f, q_hi = 0.f;
-    if (w < GROUP) qkv_pair(a, b, (kvh * GROUP + w) * D + lane, q_lo, q_hi);
     KVRegs ra, rb;
     // Split ranges are always whole (only the last live split is partial), so
     // with several splits each wave streams one contiguous quarter of its
@@ -204,29 +237,39 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
     const bool contig = a.splits > 1;
     const int wq = split_len(range_end - begin, WAVES);
     const int first = contig ? begin + w * wq : begin + w * BLK;
-    if (first < range_end) load_kv(ra, kbase, vbase, first, range_end - 1, lane);
+    load_kv(ra, kbase, vbase, first, range_end - 1, lane);  // rows clamp into the range
+    const int qidx = (kvh * GROUP + min(w, GROUP - 1)) * D + lane;
+    const int kidx = a.Hq * D + kvh * D + lane;
+    const int vidx = (a.Hq + a.Hkv) * D + kvh * D + lane;
+    QkvRaw<QP> qr, kr, vr;
+    qkv_issue(a, b, qidx, qr);
+    qkv_issue(a, b, kidx, kr);
+    qkv_issue(a, b, vidx, vr);
+    const Pair16 qg = pair16(a.q_norm_w, lane), kg = pair16(a.k_norm_w, lane);
 
     const bool bad_pos = pos_raw < 0 || pos_raw >= a.capacity;
     const int pos = bad_pos ? 0 : pos_raw;
     // Out-of-range position (a caller bug): touch no cache memory, process no keys.
     const int end = bad_pos ? begin : min(range_end, pos + 1);
     const bool owner = !bad_pos && begin <= pos && pos < end;
+    const Pair16 cr = pair16(a.cos_t + (int64_t)pos * D, lane), sr = pair16(a.sin_t + (int64_t)pos * D, lane);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const bf16_t* cosr = a.cos_t + (int64_t)pos * D;
-    const bf16_t* sinr = a.sin_t + (int64_t)pos * D;
     if (begin < end) {
         // Query head kvh*4 + w: RMSNorm + RoPE into LDS.
         uint32_t lo, hi;
         if (w < GROUP) {
-            norm_rope_pair(q_lo, q_hi, a.q_norm_w, cosr, sinr, a.eps, lane, lo, hi);
+            float q_lo, q_hi;
+            qkv_finish(a, b, qidx, qr, q_lo, q_hi);
+            norm_rope_pair(q_lo, q_hi, qg, cr, sr, a.eps, lo, hi);
             qs[w][lane] = (bf16_t)lo;
             qs[w][lane + 64] = (bf16_t)hi;
         }
         if (owner && w == 0) {
             // This token's key: normalised, rotated, appended (fused.py:553-617).
             float k_lo, k_hi;
-            qkv_pair(a, b, a.Hq * D + kvh * D + lane, k_lo, k_hi);
-            norm_rope_pair(k_lo, k_hi, a.k_norm_w, cosr, sinr, a.eps, lane, lo, hi);
+            qkv_finish(a, b, kidx, kr, k_lo, k_hi);
+            norm_rope_pair(k_lo, k_hi, kg, cr, sr, a.eps, lo, hi);
             knew[lane] = (bf16_t)lo;
             knew[lane + 64] = (bf16_t)hi;
             bf16_t* dst = a.cache_k + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
@@ -235,7 +278,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
         }
         if (owner && w == 1) {
             float v_lo, v_hi;
-            qkv_pair(a, b, (a.Hq + a.Hkv) * D + kvh * D + lane, v_lo, v_hi);
+            qkv_finish(a, b, vidx, vr, v_lo, v_hi);
             const bf16_t v0 = (bf16_t)f2bf(v_lo), v1 = (bf16_t)f2bf(v_hi);
             vnew[lane] = v0;
             vnew[lane + 64] = v1;
@@ -525,10 +568,18 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
                  part_acc, part_ml, out, Hq, Hkv, capacity, splits, eps, scale};
     const long groups = (long)splits * Hkv * B;
     const int per = split_len(capacity, splits);
-    if (groups <= 256 && per >= 8 * BLK)
-        Q3_LAUNCH(attn_decode_kernel<8>, dim3(splits, Hkv, B), dim3(8 * 64), 0, stream, a);
-    else
-        Q3_LAUNCH(attn_decode_kernel<4>, dim3(splits, Hkv, B), dim3(4 * 64), 0, stream, a);
+    const bool wide = groups <= 256 && per >= 8 * BLK;
+    const dim3 grid(splits, Hkv, B);
+    const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
+#define Q3_ATT(QPV)                                                                          \
+    do {                                                                                     \
+        if (wide) Q3_LAUNCH((attn_decode_kernel<8, QPV>), grid, dim3(8 * 64), 0, stream, a); \
+        else Q3_LAUNCH((attn_decode_kernel<4, QPV>), grid, dim3(4 * 64), 0, stream, a);      \
+    } while (0)
+    if (qp == 0) Q3_ATT(0);
+    else if (qp == 1) Q3_ATT(1);
+    else Q3_ATT(2);
+#undef Q3_ATT
     Q3_CHECK_LAUNCH();
 }
 
