@@ -384,6 +384,40 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const float* part_acc, co
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int64_t base = ((int64_t)b * Hq + h) * splits;
     float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+    if (splits <= CH) {
+        // One chunk: every (max, sum) pair and accumulator is requested at
+        // once (indices past the count re-read the last split and are
+        // masked), then the same fold as below.
+        float av[CH], mv[CH], lv[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int64_t p = base + min(j, splits - 1);
+            av[j] = part_acc[p * D + d];
+            mv[j] = part_ml[2 * p];
+            lv[j] = part_ml[2 * p + 1];
+        }
+        float cm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            if (j < splits && lv[j] > 0.f) cm = fmaxf(cm, mv[j]);
+        if (cm != -INFINITY) {
+            const float m_new = fmaxf(m_run, cm);
+            const float scale = expf(m_run - m_new);
+            acc *= scale;
+            l_run *= scale;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const float ls = j < splits ? lv[j] : 0.f;
+                if (ls > 0.f) {
+                    const float wt = expf(mv[j] - m_new);
+                    acc += av[j] * wt;
+                    l_run += ls * wt;
+                }
+            }
+        }
+        out[((int64_t)b * Hq + h) * D + d] = (bf16_t)f2bf(l_run > 0.f ? acc / l_run : 0.f);
+        return;
+    }
     for (int s0 = 0; s0 < splits; s0 += 256) {
         const int n = min(256, splits - s0);
         __syncthreads();
