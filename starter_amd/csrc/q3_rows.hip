@@ -253,17 +253,19 @@ __global__ __launch_bounds__(FIN_THREADS) void argmax_finish_kernel(const float*
     const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int p0 = threadIdx.x; p0 < nparts; p0 += 4 * FIN_THREADS) {
-        float v[4];
-        int ix[4];
+    // Eight partials per thread per round, all requested before any compare;
+    // indices past the end re-read the last partial (a duplicate never wins).
+    for (int p0 = threadIdx.x; p0 < nparts; p0 += 8 * FIN_THREADS) {
+        float v[8];
+        int ix[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = p0 + j * FIN_THREADS;
-            v[j] = p < nparts ? pv[p * B + b] : -INFINITY;
-            ix[j] = p < nparts ? pi[p * B + b] : 0x7fffffff;
+        for (int j = 0; j < 8; ++j) {
+            const int p = min(p0 + j * FIN_THREADS, nparts - 1);
+            v[j] = pv[p * B + b];
+            ix[j] = pi[p * B + b];
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 8; ++j)
             if (better(v[j], ix[j], bv, bi)) { bv = v[j]; bi = ix[j]; }
     }
 #pragma unroll
