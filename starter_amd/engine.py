@@ -75,7 +75,7 @@ SKINNY_BATCH_MAX = 64
 #: One sequence decodes in a single persistent kernel per step
 #: (``q3_decode_persistent``) when the shapes allow it; False keeps the
 #: kernel-per-op step (tests compare the two).  Off by default until the
-#: one-kernel step is the faster of the two (2.03 vs 1.98 ms per step at
+#: one-kernel step is the faster of the two (2.05 vs 1.86 ms per step at
 #: config 2 so far).  Environment override: Q3_PERSISTENT_DECODE=0 / 1.
 PERSISTENT_DECODE = os.environ.get("Q3_PERSISTENT_DECODE", "0") != "0"
 
