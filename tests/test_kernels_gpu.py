@@ -170,8 +170,10 @@ def check_projection(got, x, w, frac=0.03):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("N,K", [(1536, 320), (320, 1024), (2560, 2560), (2560, 9728)])
+@pytest.mark.parametrize("N,K", [(1536, 320), (320, 1024), (2560, 2560), (2560, 9728), (330, 1024), (2570, 4096)])
 def test_gemv_plain_store(M, N, K):
+    """N = 330 and 2570 leave waves past the last row in the last workgroup:
+    they load clamped rows and store nothing."""
     x, w = rnd((M, K), 1.0, M), rnd((N, K), 0.02, N + K)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     call("q3_gemv", _lib.X_PLAIN, P(dv(x)), K, None, None, 0.0, None, P(dv(w)), M, N, K,
@@ -218,6 +220,33 @@ def test_gemv_epilogues_and_norm_prologue(M):
     torch.cuda.synchronize()
     gu = gu.cpu()
     assert_nearly_exact(act, oc.swiglu(gu[:, 0::2], gu[:, 1::2]), frac=5e-3)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_ragged_swiglu_and_argmax(M):
+    """Row counts that leave idle waves in the last workgroup (SwiGLU: 4 rows per
+    wave; argmax: 4 rows per wave) give the same bits as the unfused path."""
+    K, I, V = 2560, 510, 4100
+    src = dv(rnd((M, K), 1.0, 31))
+    g = dv((1 + rnd((K,), 0.2, 32).float()).to(torch.bfloat16))
+    wgu = dv(rnd((2 * I, K), 0.02, 33))
+    gu = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=DEV)
+    gemv(_lib.X_NORM, src, K, wgu, M, 2 * I, K, _lib.EPI_STORE, gu, 2 * I, norm_w=g)
+    act = torch.empty(M, I, dtype=torch.bfloat16, device=DEV)
+    gemv(_lib.X_NORM, src, K, wgu, M, 2 * I, K, _lib.EPI_SWIGLU, act, I, norm_w=g)
+    wv = dv(rnd((V, K), 0.02, 34))
+    y = torch.empty(M, V, dtype=torch.bfloat16, device=DEV)
+    gemv(_lib.X_NORM, src, K, wv, M, V, K, _lib.EPI_STORE, y, V, norm_w=g)
+    nparts = call("q3_gemv_partials", M, V, _lib.EPI_ARGMAX)
+    pv = torch.empty(nparts, M, dtype=torch.float32, device=DEV)
+    pi = torch.empty(nparts, M, dtype=torch.int32, device=DEV)
+    gemv(_lib.X_NORM, src, K, wv, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi)
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), None, S())
+    torch.cuda.synchronize()
+    gu = gu.cpu()
+    assert_nearly_exact(act, oc.swiglu(gu[:, 0::2], gu[:, 1::2]), frac=5e-3)
+    assert tok.cpu().tolist() == y.cpu().float().argmax(-1).tolist()
 
 
 @pytest.mark.parametrize("M", [1, 4, 8])
@@ -412,7 +441,8 @@ def test_tile16_layout(N, K):
 
 
 @pytest.mark.parametrize("M", [1, 5, 9, 16, 17, 33, 64])
-@pytest.mark.parametrize("N,K", [(128, 256), (192, 768), (512, 1024), (2560, 4096), (6144, 2560), (2560, 9728)])
+@pytest.mark.parametrize("N,K", [(128, 256), (192, 768), (512, 1024), (2560, 4096), (6144, 2560), (2560, 9728),
+                                 (19456, 2560)])
 def test_skinny(M, N, K):
     """Weight-streaming MFMA projection (split-K + fixed-order reduce on narrow N)."""
     x, w = rnd((M, K), 1.0, M + 7), rnd((N, K), 0.02, N + K + 7)
