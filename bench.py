@@ -170,7 +170,6 @@ def main() -> int:
     from starter_amd.checkpoint import ensure_seeded_checkpoint
     from starter_amd.engine import Engine
     from starter_amd.workloads import MODEL, MODEL_SEED, WORKLOADS
-    from starter_amd._lib import call
 
     wl = WORKLOADS[args.config]
     B, P, N = wl.batch, wl.prompt, wl.new_tokens
@@ -187,10 +186,7 @@ def main() -> int:
     eng._ensure_shape(B, P, N)
     t0 = time.time()
     logits = eng._forward_prefill(ids, P)
-    with torch.cuda.stream(eng.stream):
-        call("q3_argmax_rows", logits.data_ptr(), eng.VOCAB, B, eng.VOCAB, eng.g_token.data_ptr(), None,
-             eng.stream.cuda_stream)
-        eng.g_pos.fill_(P)
+    eng._begin_decode(logits, P)
     eng.stream.synchronize()
     log(f"prefill {B}x{P} in {time.time() - t0:.2f}s")
 
@@ -205,6 +201,7 @@ def main() -> int:
         eng._decode_step()
         events[k + 1].record(eng.stream)
     torch.cuda.synchronize()
+    eng._check_step()
     ms_step = events[0].elapsed_time(events[K]) / K
     per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(K))
     ms_median = per_step[K // 2] if K % 2 else 0.5 * (per_step[K // 2 - 1] + per_step[K // 2])

@@ -162,6 +162,23 @@ int q3_attn_merge(const float *part_acc, const float *part_ml, uint16_t *out,
                   int B, int Hq, int splits, hipStream_t stream);
 /* Splits q3_attn_decode uses for a cache of `capacity` keys. */
 int q3_attn_splits(int B, int Hkv, int capacity);
+/* q3_attn_decode + q3_attn_merge in one launch (the same arithmetic, bit for
+ * bit): the split units pass their partials to merging workgroups of the same
+ * grid as flagged words in xbuf [q3_attn_xbuf_words(B, Hq, splits)] uint32,
+ * 16-byte aligned.  A word's flag names (*pos, layer), layer < 64; the caller
+ * zeroes xbuf before positions can repeat (a new prompt), so stale words never
+ * match.  Applies when q3_attn_fused_grid(B, Hq, Hkv, capacity, splits) > 0 (2..16 splits,
+ * a grid that is resident at once).  A merge that waits past 1 s sets *err = 1
+ * (err may be NULL) and writes zeros.  Replaces fused.py:729-846 (split + merge
+ * launches) with one. */
+int q3_attn_decode_fused(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
+                         const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                         const uint16_t *cos_table, const uint16_t *sin_table, const int64_t *pos,
+                         uint16_t *cache_k, uint16_t *cache_v, uint32_t *xbuf, uint16_t *out,
+                         int B, int Hq, int Hkv, int capacity, int splits, int layer,
+                         float eps, float scale, int *err, hipStream_t stream);
+int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits);
+int q3_attn_xbuf_words(int B, int Hq, int splits);
 
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
  * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /

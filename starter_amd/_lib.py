@@ -45,6 +45,10 @@ SIGNATURES = {
     "q3_attn_decode": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P],
     "q3_attn_merge": [_P, _P, _P, _I, _I, _I, _P],
     "q3_attn_splits": [_I, _I, _I],
+    "q3_attn_decode_fused": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F,
+                             _P, _P],
+    "q3_attn_fused_grid": [_I, _I, _I, _I, _I],
+    "q3_attn_xbuf_words": [_I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P],
     "q3_argmax_rows": [_P, _I, _I, _I, _P, _P, _P],
@@ -62,7 +66,8 @@ SIGNATURES = {
 _RESTYPES = {"q3_error_string": ctypes.c_char_p, "q3_persist_work_bytes": ctypes.c_int64}
 
 #: entry points that return a count, not an error code
-_COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_skinny_splits", "q3_skinny_ws_floats",
+_COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words",
+           "q3_skinny_splits", "q3_skinny_ws_floats",
            "q3_persist_grid", "q3_persist_supported", "q3_persist_work_bytes", "q3_persist_trace_words"}
 
 _LIB: ctypes.CDLL | None = None

@@ -19,6 +19,7 @@
 // pairing of operands is what matters.
 #include "q3_attn_mfma.hpp"
 #include "q3_common.hpp"
+#include "q3_exchange.hpp"
 #include "q3.h"
 
 namespace {
@@ -29,6 +30,11 @@ constexpr int D = 128;
 constexpr int GROUP = 4;     // query heads per KV head
 constexpr int BLK = 32;      // keys per block
 constexpr int THREADS = 256; // 4 waves
+// Flagged partial record of one (sequence, head, split) in the fused launch:
+// 128 accumulators then (max, sum), each FP32 as two flagged words, padded to
+// 16 bytes.
+constexpr int XREC = 2 * 128 + 4 + 4;
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // LDS V tile of the prefill kernel [32 keys][128 d] BF16, 16-byte chunks
 // swizzled so the column reads for keys kappa(g, t) hit four distinct bank groups.
@@ -89,6 +95,7 @@ struct DecodeArgs {
     bf16_t* out;  // with one split: the normalised output [B, Hq*D] directly (no merge)
     int Hq, Hkv, capacity, splits;
     float eps, scale;
+    int B;  // sequences: the stride of one split of qkv_part [qkv_splits, B, ld_qkv]
 };
 
 // Elements idx and idx + 64 of sequence b's projected q|k|v row: BF16 from
@@ -112,7 +119,7 @@ __device__ __forceinline__ void qkv_issue(const DecodeArgs& a, int b, int idx, Q
         r.blo = row[0];
         r.bhi = row[64];
     } else if constexpr (QP == 1) {
-        const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;  // one split: [B, ld_qkv]
+        const int64_t stride = (int64_t)a.B * a.ld_qkv;  // one split: [B, ld_qkv]
         const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
 #pragma unroll
         for (int j = 0; j < QKV_FAST; ++j) {
@@ -140,7 +147,7 @@ __device__ __forceinline__ void qkv_finish(const DecodeArgs& a, int b, int idx, 
                 shi += r.hi[j];
             }
     } else {
-        const int64_t stride = (int64_t)gridDim.z * a.ld_qkv;
+        const int64_t stride = (int64_t)a.B * a.ld_qkv;
         const float* base = a.qkv_part + (int64_t)b * a.ld_qkv + idx;
         for (int s0 = 0; s0 < a.qkv_splits; ++s0) {
             slo += base[(int64_t)s0 * stride];
@@ -205,9 +212,8 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // of tiles) when the grid leaves CUs idle and every wave still gets a block:
 // twice the loads in flight per (sequence, KV head).
 template <int WAVES, int QP>
-__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kvh, int b, uint32_t* xbuf, uint32_t F) {
     static_assert(WAVES == 4 || WAVES == 8, "four or eight waves");
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
 
@@ -359,17 +365,121 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
             }
         }
         const int qh = kvh * GROUP + h;
+        const int64_t p = ((int64_t)b * a.Hq + qh) * a.splits + split;
+        if (xbuf != nullptr) {  // flagged record for the merging workgroups of the same launch
+            const auto rs = q3x::rsrc(xbuf);
+            const int off = (int)p * XREC * 4;
+            u32x2_t v = {q3x::fhi(sacc, F), q3x::flo(sacc, F)};
+            __builtin_amdgcn_raw_buffer_store_b64(v, rs, off + 8 * d, 0, q3x::SC1);
+            if (d == 0) {
+                const u32x4_t ml = {q3x::fhi(M, F), q3x::flo(M, F), q3x::fhi(sl, F), q3x::flo(sl, F)};
+                q3x::st_coh(rs, off + 4 * 2 * D, ml);
+            }
+            continue;
+        }
         if (a.out != nullptr) {  // one split: what attn_merge_kernel would write
             a.out[((int64_t)b * a.Hq + qh) * D + d] = (bf16_t)f2bf(sl > 0.f ? sacc / sl : 0.f);
             continue;
         }
-        const int64_t p = ((int64_t)b * a.Hq + qh) * a.splits + split;
         a.part_acc[p * D + d] = sacc;
         if (d == 0) {
             a.part_ml[2 * p] = M;
             a.part_ml[2 * p + 1] = sl;
         }
     }
+}
+
+template <int WAVES, int QP>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(DecodeArgs a) {
+    attn_unit<WAVES, QP>(a, blockIdx.x, blockIdx.y, blockIdx.z, nullptr, 0);
+}
+
+// Attention and split merge in one launch (several splits, small grids).  The
+// first splits * Hkv * B workgroups are the attention units above (the wave
+// count q3_attn_decode would use, so the partials are the same bits); each
+// stores its partial record -- 128 accumulators and (max, sum), every FP32 as
+// two flagged words -- past the XCD-private L2.  The last Hq * B / (WAVES / 2)
+// workgroups merge WAVES / 2 heads each: they re-read the records of every split until all
+// words carry this (position, layer)'s flag, then fold them exactly as
+// attn_merge_kernel does.  The whole grid is resident at once (the launcher
+// caps it), so a merging workgroup never waits on a unit that cannot start;
+// its wait is still bounded (1 s), after which it writes zeros and sets *err.
+template <int WAVES, int QP>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(DecodeArgs a, uint32_t* xbuf, int layer,
+                                                                          int* err) {
+    constexpr int HPW = WAVES / 2;                      // heads per merging workgroup (128 threads each)
+    const int per_seq = a.splits * a.Hkv + a.Hq / HPW;  // workgroups per sequence
+    const int n_att = a.splits * a.Hkv * (int)(gridDim.x / per_seq);
+    const int pos_raw = (int)*a.pos;
+    const uint32_t F = 1u + ((uint32_t)pos_raw * 64u + (uint32_t)layer) % 65535u;
+    const int bid = blockIdx.x;
+    if (bid < n_att) {
+        const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
+        attn_unit<WAVES, QP>(a, split, kvh, b, xbuf, F);
+        return;
+    }
+    // Merge: heads HPW mi .. HPW mi + HPW - 1 of sequence b; thread t takes
+    // (head t / 128, d = t % 128).
+    constexpr int CH = 16;
+    const int mi = bid - n_att, hp = a.Hq / HPW;
+    const int b = mi / hp, h = HPW * (mi % hp) + (int)(threadIdx.x >> 7), d = threadIdx.x & 127;
+    const int S = a.splits;
+    const auto rs = q3x::rsrc(xbuf);
+    const uint32_t Fs = F << 16;
+    float av[CH], mv[CH], lv[CH];
+    q3x::SpinBound sb;
+    bool ok = true;
+    for (;;) {
+        u32x2_t aw[CH];
+        u32x4_t mw[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int off = (((b * a.Hq + h) * S + min(j, S - 1)) * XREC) * 4;
+            aw[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, off + 8 * d, 0, q3x::SC1);
+            mw[j] = q3x::ld_coh(rs, off + 4 * 2 * D);
+        }
+        uint32_t bad = 0;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            bad |= ((aw[j].x ^ Fs) | (aw[j].y ^ Fs)) & 0xffff0000u;
+            bad |= q3x::unflagged(mw[j], Fs);
+            av[j] = q3x::funpack(aw[j].x, aw[j].y);
+            mv[j] = q3x::funpack(mw[j].x, mw[j].y);
+            lv[j] = q3x::funpack(mw[j].z, mw[j].w);
+        }
+        if (__all(bad == 0)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (!sb.ok(q3x::SPIN_LIMIT)) {
+            ok = false;
+            break;
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+    if (ok) {
+        // The fold of attn_merge_kernel for one chunk of up to CH splits.
+        float cm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            if (j < S && lv[j] > 0.f) cm = fmaxf(cm, mv[j]);
+        if (cm != -INFINITY) {
+            const float m_new = fmaxf(m_run, cm);
+            const float scale = expf(m_run - m_new);
+            acc *= scale;
+            l_run *= scale;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const float ls = j < S ? lv[j] : 0.f;
+                if (ls > 0.f) {
+                    const float wt = expf(mv[j] - m_new);
+                    acc += av[j] * wt;
+                    l_run += ls * wt;
+                }
+            }
+        }
+    } else if (err != nullptr && (threadIdx.x & 63) == 0) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    a.out[((int64_t)b * a.Hq + h) * D + d] = (bf16_t)f2bf(l_run > 0.f ? acc / l_run : 0.f);
 }
 
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
@@ -570,6 +680,13 @@ __global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, 
 
 }  // namespace
 
+// Waves per attention workgroup: eight (one workgroup per CU, 128 KB of tiles)
+// when the grid leaves CUs idle and every wave still gets a block.
+static int attn_waves(int B, int Hkv, int capacity, int splits) {
+    const long groups = (long)splits * Hkv * B;
+    return groups <= 256 && split_len(capacity, splits) >= 8 * BLK ? 8 : 4;
+}
+
 extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     // One split (no merge launch: the kernel writes the output) once there are
     // enough (sequence, KV head) pairs to occupy half the CUs at moderate
@@ -599,10 +716,8 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
         !pos || !cache_k || !cache_v || (out ? splits != 1 : (!part_acc || !part_ml)))
         return (int)hipErrorInvalidValue;
     DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
-                 part_acc, part_ml, out, Hq, Hkv, capacity, splits, eps, scale};
-    const long groups = (long)splits * Hkv * B;
-    const int per = split_len(capacity, splits);
-    const bool wide = groups <= 256 && per >= 8 * BLK;
+                 part_acc, part_ml, out, Hq, Hkv, capacity, splits, eps, scale, B};
+    const bool wide = attn_waves(B, Hkv, capacity, splits) == 8;
     const dim3 grid(splits, Hkv, B);
     const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
 #define Q3_ATT(QPV)                                                                          \
@@ -614,6 +729,45 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
     else if (qp == 1) Q3_ATT(1);
     else Q3_ATT(2);
 #undef Q3_ATT
+    Q3_CHECK_LAUNCH();
+}
+
+// Grid of the fused attention + merge launch, or 0 when it does not apply:
+// several splits (at most 16, the merge's one-pass width) and a grid small
+// enough to be resident at once with room to spare (two workgroups per CU fit).
+extern "C" int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits) {
+    if (splits < 2 || splits > 16 || Hq % 4 || B < 1 || Hkv < 1 || capacity < 1) return 0;
+    const int hpw = attn_waves(B, Hkv, capacity, splits) / 2;
+    const long grid = (long)B * (splits * Hkv + Hq / hpw);
+    return grid <= 256 ? (int)grid : 0;
+}
+
+extern "C" int q3_attn_xbuf_words(int B, int Hq, int splits) { return B * Hq * splits * XREC; }
+
+extern "C" int q3_attn_decode_fused(const bf16_t* qkv, int ld_qkv, const float* qkv_part, int qkv_splits,
+                                    const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
+                                    const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
+                                    uint32_t* xbuf, bf16_t* out, int B, int Hq, int Hkv, int capacity, int splits,
+                                    int layer, float eps, float scale, int* err, hipStream_t stream) {
+    const int grid = q3_attn_fused_grid(B, Hq, Hkv, capacity, splits);
+    if (grid == 0 || Hq != GROUP * Hkv || capacity < 1 || layer < 0 || layer >= 64 ||
+        ld_qkv < (Hq + 2 * Hkv) * D || (!qkv && !qkv_part) ||
+        (qkv_part && (qkv_splits < 1 || (reinterpret_cast<uintptr_t>(qkv_part) & 3))) || !pos || !cache_k ||
+        !cache_v || !xbuf || !out || (reinterpret_cast<uintptr_t>(xbuf) & 15))
+        return (int)hipErrorInvalidValue;
+    DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos,
+                 cache_k, cache_v, nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B};
+    const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
+    const bool wide = attn_waves(B, Hkv, capacity, splits) == 8;
+#define Q3_FUSED(QPV)                                                                                          \
+    do {                                                                                                       \
+        if (wide) Q3_LAUNCH((attn_fused_kernel<8, QPV>), dim3(grid), dim3(8 * 64), 0, stream, a, xbuf, layer, err); \
+        else Q3_LAUNCH((attn_fused_kernel<4, QPV>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);     \
+    } while (0)
+    if (qp == 0) Q3_FUSED(0);
+    else if (qp == 1) Q3_FUSED(1);
+    else Q3_FUSED(2);
+#undef Q3_FUSED
     Q3_CHECK_LAUNCH();
 }
 

@@ -79,6 +79,10 @@ SKINNY_BATCH_MAX = 64
 #: config 2 so far).  Environment override: Q3_PERSISTENT_DECODE=0 / 1.
 PERSISTENT_DECODE = os.environ.get("Q3_PERSISTENT_DECODE", "0") != "0"
 
+#: Decode attention and its split merge in one launch where the grid allows it
+#: (``q3_attn_decode_fused``); False keeps two launches (tests compare them).
+FUSED_ATTENTION = os.environ.get("Q3_FUSED_ATTENTION", "1") != "0"
+
 
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
@@ -259,6 +263,14 @@ class Engine:
         self.act = self._empty(B, self.INTER)
         self.part_acc = self._empty(B, self.HEADS, self.splits, D, dtype=torch.float32)
         self.part_ml = self._empty(B, self.HEADS, self.splits, 2, dtype=torch.float32)
+        # Attention and its split merge in one launch when the grid is small
+        # enough (batch 1-4 at moderate context): flagged exchange words, zeroed
+        # at the start of every call, and a timeout word checked every step.
+        self.attn_fused = (FUSED_ATTENTION and self.splits > 1 and
+                           call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity, self.splits) > 0)
+        words = call("q3_attn_xbuf_words", B, self.HEADS, self.splits) if self.attn_fused else 4
+        self.attn_x = torch.zeros(words, dtype=torch.int32, device=self.device)
+        self.attn_err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.small = B <= GEMV_BATCH_MAX
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
         self.persist = B == 1 and PERSISTENT_DECODE and self._persist_setup(capacity)
@@ -385,12 +397,7 @@ class Engine:
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
-            call("q3_attn_decode", qkv, self.qkv_size, None, 0, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
-                 _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
-                 attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
-            if self.splits > 1:
-                call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+            self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride, vc0 + i * layer_stride)
             if self.small:
                 call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
                      B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
@@ -436,12 +443,7 @@ class Engine:
              self.EPS, s)
         for i, L in enumerate(self.layers):
             call("q3_skinny_partials", nbuf, H, T(L["qkv"]), B, self.qkv_size, H, ws, s)
-            call("q3_attn_decode", None, self.qkv_size, ws, s_qkv, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
-                 _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                 vc0 + i * layer_stride, _ptr(self.part_acc), _ptr(self.part_ml),
-                 attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
-            if self.splits > 1:
-                call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+            self._attention(i, L, (None, self.qkv_size, ws, s_qkv), kc0 + i * layer_stride, vc0 + i * layer_stride)
             call("q3_skinny_partials", attn, self.q_size, T(L["o"]), B, H, self.q_size, ws, s)
             call("q3_add_rmsnorm_partials", ws, s_o, resid, _ptr(L["post_ln"]), nbuf, B, H, self.EPS, s)
             call("q3_skinny_tiled", nbuf, H, T(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, ws, s)
@@ -451,6 +453,22 @@ class Engine:
         call("q3_skinny_argmax", nbuf, H, T(self.lm_head), B, V, H, _ptr(self.logits) if self.keep_logits else None,
              V, _ptr(self.part_val), _ptr(self.part_idx), s)
         call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
+
+    def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int) -> None:
+        """Layer i's decode attention into attn_out: q/k norm + RoPE + KV append,
+        split-K GQA and the split merge (one launch when ``attn_fused``).
+        ``src`` is (qkv, ld, qkv partials, partial count)."""
+        B, Hq, Hkv, C, s = self.batch, self.HEADS, self.KV_HEADS, self.capacity, self._s
+        pos, attn = _ptr(self.g_pos), _ptr(self.attn_out)
+        common = (_ptr(L["q_norm"]), _ptr(L["k_norm"]), _ptr(self.cos_table), _ptr(self.sin_table), pos, kc, vc)
+        if self.attn_fused:
+            call("q3_attn_decode_fused", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i,
+                 self.EPS, self.SCALE, _ptr(self.attn_err), s)
+            return
+        call("q3_attn_decode", *src, *common, _ptr(self.part_acc), _ptr(self.part_ml),
+             attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
+        if self.splits > 1:
+            call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
 
     def _proj(self, x: int, ldx: int, w: torch.Tensor, N: int, K: int, epi: int, y: int, ldy: int) -> None:
         """Decode projection for batches outside the GEMV and fused MFMA paths (more
@@ -467,6 +485,7 @@ class Engine:
             for _ in range(2):
                 self.g_pos.fill_(max(0, self.capacity - 2))
                 self.g_token.zero_()
+                self._clear_exchange()
                 self._enqueue_decode()
             self.g_pos.zero_()
             self.g_token.zero_()
@@ -486,6 +505,22 @@ class Engine:
         self.graph = exec_ptr.value
         _log(f"decode graph captured (batch={self.batch}, splits={self.splits})")
 
+    def _clear_exchange(self) -> None:
+        """Zero the fused attention's exchange words and timeout word on the
+        decode stream.  Its flags are derived from (position, layer), so words
+        left by an earlier call at the same positions would read as fresh."""
+        self.attn_x.zero_()
+        self.attn_err.zero_()
+
+    def _begin_decode(self, logits: torch.Tensor, seq_len: int) -> None:
+        """First token = argmax of the prefill's last logits; positions restart
+        at the prompt length (reference ``engine/engine.py:1077-1079``)."""
+        with torch.cuda.stream(self.stream):
+            call("q3_argmax_rows", _ptr(logits), self.VOCAB, self.batch, self.VOCAB, _ptr(self.g_token), None,
+                 self._s)
+            self.g_pos.fill_(seq_len)
+            self._clear_exchange()
+
     def _decode_step(self) -> torch.Tensor:
         """Replay the captured step: g_token <- next token, g_pos += 1."""
         call("q3_graph_launch", self.graph, self._s)
@@ -495,6 +530,12 @@ class Engine:
         """The one-kernel step reports a launch that could not complete (a wait
         past its time bound) as token -1; raise, and drop the step's state so the
         next call rebuilds it."""
+        if self.attn_fused:
+            if int(self.attn_err.cpu()[0]):
+                self.graph_key_reset()
+                raise RuntimeError("q3_attn_decode_fused did not complete: a merge workgroup waited "
+                                   "past its time bound")
+            return
         if not self.persist:
             return
         if tokens is None:
@@ -608,10 +649,7 @@ class Engine:
         # No state carries between calls: positions restart at the prompt length,
         # and only slots below the running position are ever read.
         logits = self._forward_prefill(ids, seq_len)
-        with torch.cuda.stream(self.stream):
-            call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
-                 self._s)
-            self.g_pos.fill_(seq_len)
+        self._begin_decode(logits, seq_len)
         host = torch.empty(batch, dtype=torch.int64, pin_memory=True)
         done = torch.cuda.Event()
         pending = False
@@ -654,10 +692,7 @@ class Engine:
         self.graph_key_reset()
         self._ensure_shape(batch, seq_len, max_new_tokens)
         logits = self._forward_prefill(ids, seq_len)
-        with torch.cuda.stream(self.stream):
-            call("q3_argmax_rows", _ptr(logits), self.VOCAB, batch, self.VOCAB, _ptr(self.g_token), None,
-                 self._s)
-            self.g_pos.fill_(seq_len)
+        self._begin_decode(logits, seq_len)
         self.stream.synchronize()
         steps, kept = [self.g_token.cpu().tolist()], [logits.view(batch, -1).cpu()]
         for i in range(max_new_tokens - 1):

@@ -137,6 +137,38 @@ def test_fused_mfma_decode_matches_oracle(tile_engine, tile_ckpt, batch):
     assert list(tile_engine.generate(ids, 6)) == steps
 
 
+def _trace_attention(engine, ids, n, fused):
+    saved = engine_mod.FUSED_ATTENTION
+    engine_mod.FUSED_ATTENTION = fused
+    try:
+        steps, logits = engine.trace_logits(ids, n)
+        assert engine.attn_fused == fused
+        tokens = list(engine.generate(ids, n))
+        assert int(engine.attn_err.cpu()[0]) == 0
+    finally:
+        engine_mod.FUSED_ATTENTION = saved
+    return steps, logits, tokens
+
+
+@pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700), (4, 260), (5, 300)])
+def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, batch, prompt):
+    """Contexts long enough for split attention (2..16 splits, grid within one
+    wave of workgroups) run attention and its split merge as one launch.  Same
+    bits as the two-launch path at every step, for trace_logits and generate,
+    across repeated calls (the exchange words are cleared per call), and the
+    oracle's stream.  Batch 5 takes the MFMA (tiled-weight) step."""
+    cfg, tensors = load_checkpoint(tile_ckpt)
+    rng = np.random.Generator(np.random.PCG64(900 + batch))
+    ids = rng.integers(0, cfg.vocab_size, (batch, prompt)).tolist()
+    f_steps, f_logits, f_tokens = _trace_attention(tile_engine, ids, 8, True)
+    s_steps, s_logits, s_tokens = _trace_attention(tile_engine, ids, 8, False)
+    assert torch.equal(f_logits, s_logits)
+    assert f_steps == s_steps == f_tokens == s_tokens
+    orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
+    want, want_logits = orc.generate(ids, 8, keep_logits=True)
+    check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
+
+
 def test_batch_rows_are_independent(tiny_engine):
     """A row's tokens do not depend on the other rows of the batch (bit-identical)."""
     rng = np.random.Generator(np.random.PCG64(3))

@@ -532,6 +532,53 @@ def test_add_rmsnorm_partials(M, N, K):
     assert not torch.equal(r2.cpu(), res)
 
 
+@pytest.mark.parametrize("B,C,pos,splits,qsplits", [(1, 1536, 1100, 12, 0), (1, 1536, 1535, 12, 0),
+                                                    (2, 700, 255, 3, 0), (4, 1536, 1000, 6, 0),
+                                                    (1, 300, 0, 2, 0), (1, 64, 63, 2, 0), (3, 900, 640, 5, 3),
+                                                    (1, 2000, 1999, 16, 9)])
+def test_attn_decode_fused(B, C, pos, splits, qsplits):
+    """Attention + merge in one launch == q3_attn_decode then q3_attn_merge, bit
+    for bit, over several layers' flags; a zeroed exchange buffer makes a
+    repeated (position, layer) safe."""
+    Hq, Hkv, D = 32, 8, 128
+    width = (Hq + 2 * Hkv) * D
+    assert call("q3_attn_fused_grid", B, Hq, Hkv, C, splits) > 0
+    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    posd = dv(torch.tensor([pos]))
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for layer, seed in ((0, 7), (1, 8), (0, 9)):
+        if layer == 0 and seed == 9:
+            xbuf.zero_()  # the same (position, layer) as the first round
+        if qsplits:
+            part = (torch.randn(qsplits, B, width, generator=torch.Generator().manual_seed(seed)) * 0.7).float()
+            src = (None, width, P(dv(part)), qsplits)
+        else:
+            src = (P(dv(rnd((B, width), 1.5, seed))), width, None, 0)
+        outs, caches = [], []
+        for fused in (False, True):
+            ckd, cvd = dv(ck), dv(cv)
+            out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+            if fused:
+                call("q3_attn_decode_fused", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd),
+                     P(ckd), P(cvd), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5, P(err), S())
+            else:
+                pacc = torch.empty(B, Hq, splits, D, dtype=torch.float32, device=DEV)
+                pml = torch.empty(B, Hq, splits, 2, dtype=torch.float32, device=DEV)
+                call("q3_attn_decode", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd), P(ckd),
+                     P(cvd), P(pacc), P(pml), None, B, Hq, Hkv, C, splits, 1e-6, D ** -0.5, S())
+                call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, splits, S())
+            torch.cuda.synchronize()
+            outs.append(out.cpu())
+            caches.append((ckd.cpu(), cvd.cpu()))
+        assert torch.equal(outs[0], outs[1]), (layer, seed)
+        assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    assert err.item() == 0
+
+
 @pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6)])
 def test_attn_decode_qkv_partials(B, C, pos, qsplits):
     """q/k/v from FP32 split partials == from their in-order sum rounded to BF16, bit for bit."""
