@@ -61,13 +61,13 @@ def test_bad_arguments_raise_without_launching():
 
 def test_attention_splits_policy():
     # One split from 128 (sequence, KV head) pairs at moderate context or 512 at any;
-    # else about 512 workgroups of >= 256 keys, 128-key splits while CUs would idle.
+    # else about 512 workgroups (768 from 64 pairs) of >= 256 keys, 128-key splits while CUs would idle.
     assert _lib.call("q3_attn_splits", 1, 8, 64) == 1
     assert _lib.call("q3_attn_splits", 1, 8, 1536) == 12
     assert _lib.call("q3_attn_splits", 16, 8, 768) == 1
-    assert _lib.call("q3_attn_splits", 16, 8, 16384) == 4
+    assert _lib.call("q3_attn_splits", 16, 8, 16384) == 6
     assert _lib.call("q3_attn_splits", 64, 8, 2176) == 1
-    assert _lib.call("q3_attn_splits", 8, 8, 16512) == 8
+    assert _lib.call("q3_attn_splits", 8, 8, 16512) == 12
     assert _lib.call("q3_attn_splits", 4, 8, 1536) == 6
     assert _lib.call("q3_attn_splits", 200, 8, 100) == 1
 
