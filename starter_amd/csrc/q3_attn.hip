@@ -736,14 +736,42 @@ extern "C" int q3_attn_decode(const bf16_t* qkv, int ld_qkv, const float* qkv_pa
     Q3_CHECK_LAUNCH();
 }
 
+// Workgroups of the (four-wave) fused kernel that are resident at once on the
+// current device: the occupancy of its least-occupying q|k|v-source variant
+// times the CU count (0 if unknown).  Cached per device.
+static int fused_resident() {
+    constexpr int MAX_DEV = 64;
+    static int cached[MAX_DEV];  // 0 = not yet asked; -1 = unknown
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    if (cached[dev] != 0) return cached[dev] > 0 ? cached[dev] : 0;
+    int cus = 0, per = 1 << 30;
+    bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
+    for (const void* f : {reinterpret_cast<const void*>(attn_fused_kernel<4, 0>),
+                          reinterpret_cast<const void*>(attn_fused_kernel<4, 1>),
+                          reinterpret_cast<const void*>(attn_fused_kernel<4, 2>)}) {
+        int n = 0;
+        ok = ok && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 4 * 64, 0) == hipSuccess;
+        per = n < per ? n : per;
+    }
+    ok = ok && per >= 1;
+    cached[dev] = ok ? per * cus : -1;
+    return ok ? per * cus : 0;
+}
+
 // Grid of the fused attention + merge launch, or 0 when it does not apply:
-// several splits (at most 16, the merge's one-pass width) and a grid small
-// enough to be resident at once with room to spare (two workgroups per CU fit).
+// several splits (at most 16, the merge's one-pass width), four-wave attention
+// workgroups, and a grid that is resident at once (every merge workgroup then
+// waits only for workgroups that are running).  Where the attention takes
+// eight-wave workgroups (one per CU: 130 KB of LDS), the merge workgroups
+// measured slower than a merge launch (B=3 and 4 at 1536 keys, 6 splits:
+// +0.3-0.4 us; B=1 at 4096 keys, 16 splits: +0.7 us), while four-wave shapes
+// gain (B=1 at 1536 keys, 12 splits: 10.52 -> 9.99 us; B=2: 10.99 -> 10.35).
 extern "C" int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits) {
-    if (splits < 2 || splits > 16 || Hq % 4 || B < 1 || Hkv < 1 || capacity < 1) return 0;
-    const int hpw = attn_waves(B, Hkv, capacity, splits) / 2;
-    const long grid = (long)B * (splits * Hkv + Hq / hpw);
-    return grid <= 256 ? (int)grid : 0;
+    if (splits < 2 || splits > 16 || Hq % 2 || B < 1 || Hkv < 1 || capacity < 1) return 0;
+    if (attn_waves(B, Hkv, capacity, splits) != 4) return 0;
+    const long grid = (long)B * (splits * Hkv + Hq / 2);
+    return grid <= fused_resident() ? (int)grid : 0;
 }
 
 extern "C" int q3_attn_xbuf_words(int B, int Hq, int splits) { return B * Hq * splits * XREC; }
@@ -762,16 +790,9 @@ extern "C" int q3_attn_decode_fused(const bf16_t* qkv, int ld_qkv, const float* 
     DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos,
                  cache_k, cache_v, nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B};
     const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
-    const bool wide = attn_waves(B, Hkv, capacity, splits) == 8;
-#define Q3_FUSED(QPV)                                                                                          \
-    do {                                                                                                       \
-        if (wide) Q3_LAUNCH((attn_fused_kernel<8, QPV>), dim3(grid), dim3(8 * 64), 0, stream, a, xbuf, layer, err); \
-        else Q3_LAUNCH((attn_fused_kernel<4, QPV>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);     \
-    } while (0)
-    if (qp == 0) Q3_FUSED(0);
-    else if (qp == 1) Q3_FUSED(1);
-    else Q3_FUSED(2);
-#undef Q3_FUSED
+    if (qp == 0) Q3_LAUNCH((attn_fused_kernel<4, 0>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
+    else if (qp == 1) Q3_LAUNCH((attn_fused_kernel<4, 1>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
+    else Q3_LAUNCH((attn_fused_kernel<4, 2>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
     Q3_CHECK_LAUNCH();
 }
 

@@ -532,10 +532,22 @@ def test_add_rmsnorm_partials(M, N, K):
     assert not torch.equal(r2.cpu(), res)
 
 
+def test_attn_fused_applies_to_four_wave_shapes():
+    """The fused launch takes shapes whose attention runs four-wave workgroups
+    and whose grid is resident at once; eight-wave shapes keep two launches."""
+    assert call("q3_attn_fused_grid", 1, 32, 8, 1536, 12) == 1 * (12 * 8 + 16)
+    assert call("q3_attn_fused_grid", 4, 32, 8, 1536, 6) == 0     # 256 keys per split: eight waves
+    assert call("q3_attn_fused_grid", 1, 32, 8, 4096, 16) == 0    # likewise
+    assert call("q3_attn_fused_grid", 1, 32, 8, 1536, 1) == 0
+    assert call("q3_attn_fused_grid", 1, 32, 8, 1536, 17) == 0
+    assert call("q3_attn_fused_grid", 4, 32, 8, 2048, 12) == 4 * (12 * 8 + 16)  # two per CU
+    assert call("q3_attn_fused_grid", 64, 32, 8, 2048, 16) == 0   # 9216 workgroups: not resident
+
+
 @pytest.mark.parametrize("B,C,pos,splits,qsplits", [(1, 1536, 1100, 12, 0), (1, 1536, 1535, 12, 0),
-                                                    (2, 700, 255, 3, 0), (4, 1536, 1000, 6, 0),
+                                                    (2, 700, 255, 4, 0), (4, 1536, 1000, 8, 0),
                                                     (1, 300, 0, 2, 0), (1, 64, 63, 2, 0), (3, 900, 640, 5, 3),
-                                                    (1, 2000, 1999, 16, 9)])
+                                                    (1, 2000, 1999, 16, 9), (4, 2048, 2000, 12, 0)])
 def test_attn_decode_fused(B, C, pos, splits, qsplits):
     """Attention + merge in one launch == q3_attn_decode then q3_attn_merge, bit
     for bit, over several layers' flags; a zeroed exchange buffer makes a
