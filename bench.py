@@ -236,9 +236,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,0.02) BF16 weights, uniform random prompt ids)",
-        "config": {"workload": wl.name, "batch": B, "prompt": P, "new_tokens": N,
-                   "model": "Qwen3-4B architecture (36 layers, 2560 hidden, GQA 32/8)"},
+        "data": "synthetic (seeded N(0,0.02) BF16 weights of the Qwen3-4B shapes, uniform random prompt ids)",
+        "config": {"workload": wl.name, "batch": B, "prompt": P, "new_tokens": N},
         "step_roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes),
                           "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
