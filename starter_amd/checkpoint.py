@@ -311,12 +311,14 @@ def _read_safetensors(file: pathlib.Path) -> dict[str, tuple[np.ndarray, str]]:
 
 
 def _to_bf16_bits(arr: np.ndarray, dtype: str) -> np.ndarray:
-    """Raw BF16 bits; F32/F16 checkpoints are rounded to nearest even."""
+    """Raw BF16 bits; F32/F16 checkpoints are rounded to nearest even, and a
+    NaN stays a NaN (0x7FC0; rounding its bits could carry into infinity)."""
     if dtype == "BF16":
         return arr
     f = np.ascontiguousarray(arr, dtype=np.float32).view(np.uint32)
-    rounded = (f.astype(np.uint64) + 0x7FFF + ((f >> 16) & 1)) >> 16
-    return rounded.astype(np.uint16)
+    rounded = ((f.astype(np.uint64) + 0x7FFF + ((f >> 16) & 1)) >> 16).astype(np.uint16)
+    rounded[(f & 0x7FFFFFFF) > 0x7F800000] = 0x7FC0
+    return rounded
 
 
 def load_checkpoint(path: str | os.PathLike) -> tuple[Qwen3Config, dict[str, np.ndarray]]:

@@ -62,3 +62,86 @@ def test_prompts():
     assert all(0 <= x < 151643 for r in p for x in r)
     assert p[0] != p[1]
     assert ck.seeded_prompt(1, 2, 32) == p
+
+
+def _save(path, tensors):
+    """Write {name: uint16 BF16 bits or float32 array} with safetensors' own writer."""
+    import torch
+    from safetensors.torch import save_file
+
+    out = {}
+    for k, v in tensors.items():
+        t = torch.from_numpy(np.array(v, copy=True))
+        out[k] = t.view(torch.bfloat16) if v.dtype == np.uint16 else t
+    save_file(out, str(path))
+
+
+def test_sharded_checkpoint_loads_like_one_file(tmp_path):
+    """HF layout with model.safetensors.index.json: tensors spread over shards
+    load exactly as from one file (reference ``engine/engine.py:124-133``)."""
+    one = tmp_path / "one"
+    ck.write_seeded_checkpoint(one, TINY, seed=4, std=0.05, gain_std=0.1)
+    cfg, want = ck.load_checkpoint(one)
+    sharded = tmp_path / "sharded"
+    sharded.mkdir()
+    (sharded / "config.json").write_text((one / "config.json").read_text())
+    names = sorted(want)
+    parts = {"model-00001-of-00002.safetensors": names[::2], "model-00002-of-00002.safetensors": names[1::2]}
+    for file, keys in parts.items():
+        _save(sharded / file, {k: want[k] for k in keys})
+    weight_map = {k: f for f, keys in parts.items() for k in keys}
+    (sharded / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
+    cfg2, got = ck.load_checkpoint(sharded)
+    assert cfg2 == cfg and set(got) == set(want)
+    for k in want:
+        assert np.array_equal(got[k], want[k]), k
+
+
+def test_f32_checkpoint_rounds_to_nearest_even(tmp_path):
+    """F32 tensors become BF16 by round-to-nearest-even, as torch's cast does
+    (ties and infinities included); NaNs stay NaNs."""
+    import torch
+
+    ck.write_seeded_checkpoint(tmp_path, TINY, seed=5, std=0.05, gain_std=0.1)
+    _, bf = ck.load_checkpoint(tmp_path)
+    rng = np.random.Generator(np.random.PCG64(6))
+    f32 = {k: rng.standard_normal(v.shape).astype(np.float32) for k, v in bf.items()}
+    name = sorted(f32)[0]
+    ties = np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 3.0e38, 1e-40, np.inf, -np.inf],
+                    np.float32)
+    nans = np.array([0x7F800001, 0xFFC00000, 0x7FFFFFFF], np.uint32).view(np.float32)
+    flat = f32[name].reshape(-1)
+    flat[:ties.size] = ties
+    flat[ties.size:ties.size + nans.size] = nans
+    (tmp_path / "model.safetensors").unlink()
+    _save(tmp_path / "model.safetensors", f32)
+    _, got = ck.load_checkpoint(tmp_path)
+    for k, v in f32.items():
+        want = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        nan = np.isnan(v)
+        assert np.array_equal(got[k][~nan], want[~nan]), k
+        # NaN bit patterns differ between torch's scalar and vector casts; a NaN must stay one.
+        assert np.all((got[k][nan] & 0x7F80) == 0x7F80) and np.all(got[k][nan] & 0x7F), k
+    assert np.isnan(f32[name]).sum() == nans.size
+
+
+def test_missing_or_misshapen_tensor_raises(tmp_path):
+    import pytest
+
+    ck.write_seeded_checkpoint(tmp_path, TINY, seed=7, std=0.05, gain_std=0.1)
+    _, t = ck.load_checkpoint(tmp_path)
+    name = sorted(t)[0]
+    short = dict(t)
+    del short[name]
+    (tmp_path / "model.safetensors").unlink()
+    _save(tmp_path / "model.safetensors", short)
+    with pytest.raises(KeyError, match="checkpoint lacks"):
+        ck.load_checkpoint(tmp_path)
+    bad = dict(t)
+    bad[name] = t[name].reshape(-1)[:-1].copy()
+    (tmp_path / "model.safetensors").unlink()
+    _save(tmp_path / "model.safetensors", bad)
+    with pytest.raises(ValueError, match="has shape"):
+        ck.load_checkpoint(tmp_path)
+    with pytest.raises(FileNotFoundError):
+        ck.load_checkpoint(tmp_path / "absent")
