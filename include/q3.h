@@ -68,6 +68,21 @@ int q3_gemv_partials(int M, int N, int epi);
 int q3_gemm(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, hipStream_t stream);
 
+/* Prompt-pass projection through hipBLASLt: y = bf16(x . W^T), FP32
+ * accumulation, one rounding (F.linear -> cuBLAS, engine.py:450,803).
+ * workspace: device memory of workspace_bytes for the library (may be 0
+ * bytes).  Creates the library handle on a device's first call (allocates:
+ * not under stream capture).  hipErrorNotSupported when the library offers no
+ * algorithm for the shape within the workspace. */
+int q3_gemm_lt(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
+               uint16_t *y, int ldy, void *workspace, size_t workspace_bytes,
+               hipStream_t stream);
+
+/* act[r, j] = bf16(bf16(silu(g)) * u), (g, u) = gu[r, 2j], gu[r, 2j + 1]:
+ * swiglu (fused.py:872; engine.py:464) on interleaved gate/up rows [rows, 2I].
+ * I % 8 == 0; gu, act 16-byte aligned. */
+int q3_swiglu_rows(const uint16_t *gu, uint16_t *act, int rows, int I, hipStream_t stream);
+
 /* Decode projection for 1..64 rows on MFMA, weights streamed from HBM into
  * MFMA operands: y = epi(x . W^T), epi in {STORE, RESID, SWIGLU}.  Replaces
  * skinny_linear / skinny_linear_split (fused.py:365,525) at batch 9..64.

@@ -23,6 +23,7 @@ GEMV_MAX_NORM_K = 4096
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_Z = ctypes.c_size_t
 
 #: name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES = {
@@ -30,6 +31,8 @@ SIGNATURES = {
     "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
     "q3_gemv_partials": [_I, _I, _I],
     "q3_gemm": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P],
+    "q3_gemm_lt": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _Z, _P],
+    "q3_swiglu_rows": [_P, _P, _I, _I, _P],
     "q3_skinny": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_tiled": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_partials": [_P, _I, _P, _I, _I, _I, _P, _P],

@@ -322,6 +322,43 @@ def test_gemm(M, N, K):
     assert_nearly_exact(act, oc.swiglu(yc[:, 0::2], yc[:, 1::2]), frac=5e-3)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 320, 1024), (300, 1536, 320), (513, 2560, 2560), (2048, 6144, 2560),
+                                   (1000, 2560, 9728)])
+def test_gemm_lt(M, N, K):
+    """Prompt-pass projection through hipBLASLt: the float64 dot products of the
+    same BF16 operands, rounded once (the same bar as the MFMA GEMM), with a
+    row stride on x and y."""
+    x, w = rnd((M, K + 64), 1.0, M + 3)[:, :K], rnd((N, K), 0.02, N + K + 3)
+    xd, wd = dv(x.contiguous()), dv(w)
+    xs = dv(torch.zeros(M, K + 64, dtype=torch.bfloat16))
+    xs[:, :K] = xd
+    y = dv(torch.full((M, N + 8), 7.0, dtype=torch.bfloat16))
+    ws = dv(torch.empty(64 << 20, dtype=torch.uint8))
+    call("q3_gemm_lt", P(xs), K + 64, P(wd), M, N, K, P(y), N + 8, P(ws), 64 << 20, S())
+    torch.cuda.synchronize()
+    check_projection(y[:, :N], x, w)
+    assert torch.all(y[:, N:].cpu() == 7.0)  # the row padding is not written
+
+
+@pytest.mark.parametrize("rows,I", [(1, 8), (7, 1024), (300, 9728)])
+def test_swiglu_rows_matches_fused_epilogue(rows, I):
+    """q3_swiglu_rows on a stored gate/up projection == the GEMM's fused SwiGLU
+    epilogue, bit for bit (both round the accumulator to BF16 first)."""
+    K = 256
+    x, w = rnd((rows, K), 1.0, rows + 11), rnd((2 * I, K), 0.05, I + 12)
+    xd, wd = dv(x), dv(w)
+    gu = dv(torch.empty(rows, 2 * I, dtype=torch.bfloat16))
+    fused = dv(torch.empty(rows, I, dtype=torch.bfloat16))
+    act = dv(torch.empty(rows, I, dtype=torch.bfloat16))
+    call("q3_gemm", P(xd), K, P(wd), rows, 2 * I, K, _lib.EPI_STORE, P(gu), 2 * I, S())
+    call("q3_gemm", P(xd), K, P(wd), rows, 2 * I, K, _lib.EPI_SWIGLU, P(fused), I, S())
+    call("q3_swiglu_rows", P(gu), P(act), rows, I, S())
+    torch.cuda.synchronize()
+    assert torch.equal(act.cpu(), fused.cpu())
+    g = gu.cpu()
+    assert_nearly_exact(act, oc.swiglu(g[:, 0::2], g[:, 1::2]), frac=5e-3)
+
+
 # -------------------------------------------------------------- attention
 
 
