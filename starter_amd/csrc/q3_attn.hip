@@ -566,12 +566,15 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const float* part_acc, co
 
 // grid (ceil(T/32), Hkv, B); wave w = query head kvh*4 + w, 32 queries per
 // workgroup (two MFMA column blocks of 16).  K and V blocks of 32 keys are
-// staged in LDS once and shared by the four heads.
-__global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, const bf16_t* cache_k,
+// staged in LDS once and shared by the four heads; the next block's rows are
+// loaded into registers while the current one computes.  Workgroups start
+// with the last queries (the longest causal ranges), so the short ones fill
+// the tail of the launch.
+__global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* q, const bf16_t* cache_k,
                                                                const bf16_t* cache_v, bf16_t* out,
                                                                int T, int start, int Hq, int Hkv,
                                                                int capacity, float scale) {
-    const int qb0 = blockIdx.x * 32, kvh = blockIdx.y, b = blockIdx.z;
+    const int qb0 = (gridDim.x - 1 - blockIdx.x) * 32, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
     const int h = kvh * GROUP + w;
@@ -605,22 +608,34 @@ __global__ __launch_bounds__(THREADS) void attn_prefill_kernel(const bf16_t* q, 
 
     const int q_last = min(qb0 + 31, T - 1);
     const int key_end = start + q_last + 1;  // keys 0 .. start+q_last
-    for (int kb = 0; kb < key_end; kb += BLK) {
-        __syncthreads();
-        // 32 keys x 256 B for K and V: 512 16-byte chunks each, 2 per thread.
+    // 32 keys x 256 B for K and V: 512 16-byte chunks each, 2 per thread.
+    // Rows past key_end re-read key_end - 1 (inside the cache); every query
+    // of the workgroup masks them, so they add exactly zero.
+    u32x4_t kr[2], vr[2];
+    auto load_block = [&](int kb) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int e = tid + j * THREADS;
-            const int r = e >> 4, c = e & 15, key = kb + r;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (key < key_end) {
-                kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + 8 * c);
-                vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + 8 * c);
-            }
-            *reinterpret_cast<uint4*>(ks + r * D + k_chunk(r, c) * 8) = kv;
-            *reinterpret_cast<uint4*>(vs + r * D + v_chunk(r, c) * 8) = vv;
+            const int key = min(kb + (e >> 4), key_end - 1), c = e & 15;
+            kr[j] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + 8 * c);
+            vr[j] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + 8 * c);
+        }
+    };
+    load_block(0);
+    for (int kb = 0; kb < key_end; kb += BLK) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int e = tid + j * THREADS;
+            const int r = e >> 4, c = e & 15;
+            *reinterpret_cast<u32x4_t*>(ks + r * D + k_chunk(r, c) * 8) = kr[j];
+            *reinterpret_cast<u32x4_t*>(vs + r * D + v_chunk(r, c) * 8) = vr[j];
         }
         __syncthreads();
+        // The next block (the last one again on the final pass: rows clamp)
+        // streams in while this one computes.
+        load_block(min(kb + BLK, key_end - 1));
+        __builtin_amdgcn_sched_barrier(0);
 
         bf16x8_t kop[2][4];
 #pragma unroll
