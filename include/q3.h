@@ -195,6 +195,26 @@ int q3_attn_decode_fused(const uint16_t *qkv, int ld_qkv, const float *qkv_part,
 int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits);
 int q3_attn_xbuf_words(int B, int Hq, int splits);
 
+/* The fused launch of one sequence (B = 1) plus the o-projection that follows
+ * it: resid[r] = bf16(resid[r] + bf16(attn . o_w[r])) for r < N (o_w [N, Hq*128],
+ * Hq*128 <= 4096 and a multiple of 512).  Its workgroups load o_w while the
+ * attention runs and read the merged heads as flagged words from xo
+ * (q3_attn_xo_words(Hq) words, 16-byte aligned, zeroed at the start of every
+ * call like xbuf).  Bit-identical to q3_attn_decode_fused followed by
+ * q3_gemv(X_PLAIN, o_w, EPI_RESID).  Replaces decode_attention + the o_proj
+ * _linear with its add_norm residual (engine.py:720-732,450-456).
+ * q3_attn_fused_o_grid returns the grid, or 0 where this launch does not
+ * apply (B != 1, no fused grid, or not resident at once). */
+int q3_attn_decode_fused_o(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
+                           const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                           const uint16_t *cos_table, const uint16_t *sin_table, const int64_t *pos,
+                           uint16_t *cache_k, uint16_t *cache_v, uint32_t *xbuf, uint16_t *out,
+                           const uint16_t *o_w, int N, uint16_t *resid, uint32_t *xo, int B, int Hq,
+                           int Hkv, int capacity, int splits, int layer, float eps, float scale,
+                           int *err, hipStream_t stream);
+int q3_attn_fused_o_grid(int B, int Hq, int Hkv, int capacity, int splits, int N);
+int q3_attn_xo_words(int Hq);
+
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
  * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /
  * chunk mask (engine.py:263-280,777-787). */

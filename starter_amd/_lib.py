@@ -51,6 +51,10 @@ SIGNATURES = {
     "q3_attn_decode_fused": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F,
                              _P, _P],
     "q3_attn_fused_grid": [_I, _I, _I, _I, _I],
+    "q3_attn_decode_fused_o": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
+                               _I, _F, _F, _P, _P],
+    "q3_attn_fused_o_grid": [_I, _I, _I, _I, _I, _I],
+    "q3_attn_xo_words": [_I],
     "q3_attn_xbuf_words": [_I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P],
@@ -70,6 +74,7 @@ _RESTYPES = {"q3_error_string": ctypes.c_char_p, "q3_persist_work_bytes": ctypes
 
 #: entry points that return a count, not an error code
 _COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words",
+           "q3_attn_fused_o_grid", "q3_attn_xo_words",
            "q3_skinny_splits", "q3_skinny_ws_floats",
            "q3_persist_grid", "q3_persist_supported", "q3_persist_work_bytes", "q3_persist_trace_words"}
 

@@ -85,6 +85,11 @@ PERSISTENT_DECODE = os.environ.get("Q3_PERSISTENT_DECODE", "0") != "0"
 PREFILL_BLASLT = os.environ.get("Q3_PREFILL_BLASLT", "1") != "0"
 LT_WORKSPACE_BYTES = 64 << 20
 
+#: At batch 1, the o-projection (with its residual join) in that same launch
+#: (``q3_attn_decode_fused_o``).  Off by default: bit-identical, but measured
+#: slower at config 2 (1.875 against 1.854 ms per step).
+FUSED_O_PROJECTION = os.environ.get("Q3_FUSED_O_PROJECTION", "0") != "0"
+
 #: Decode attention and its split merge in one launch where the grid allows it
 #: (``q3_attn_decode_fused``); False keeps two launches (tests compare them).
 FUSED_ATTENTION = os.environ.get("Q3_FUSED_ATTENTION", "1") != "0"
@@ -277,6 +282,12 @@ class Engine:
                            call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity, self.splits) > 0)
         words = call("q3_attn_xbuf_words", B, self.HEADS, self.splits) if self.attn_fused else 4
         self.attn_x = torch.zeros(words, dtype=torch.int32, device=self.device)
+        # One sequence: the o-projection joins that launch too (its weights stream in
+        # while attention runs), reading the merged heads as flagged words.
+        self.attn_fused_o = (self.attn_fused and FUSED_O_PROJECTION and
+                             call("q3_attn_fused_o_grid", B, self.HEADS, Hkv, capacity, self.splits, H) > 0)
+        words = call("q3_attn_xo_words", self.HEADS) if self.attn_fused_o else 4
+        self.attn_xo = torch.zeros(words, dtype=torch.int32, device=self.device)
         self.attn_err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.small = B <= GEMV_BATCH_MAX
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
@@ -404,10 +415,12 @@ class Engine:
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
-            self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride, vc0 + i * layer_stride)
+            o_done = self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride,
+                                     vc0 + i * layer_stride, o_proj=self.small)
             if self.small:
-                call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
-                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
+                if not o_done:
+                    call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
+                         B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
                 call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["post_ln"]), self.EPS, None,
                      _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, None, None, None, s)
                 call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
@@ -461,21 +474,29 @@ class Engine:
              V, _ptr(self.part_val), _ptr(self.part_idx), s)
         call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
 
-    def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int) -> None:
+    def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int, o_proj: bool = False) -> bool:
         """Layer i's decode attention into attn_out: q/k norm + RoPE + KV append,
         split-K GQA and the split merge (one launch when ``attn_fused``).
-        ``src`` is (qkv, ld, qkv partials, partial count)."""
+        ``src`` is (qkv, ld, qkv partials, partial count).  With ``o_proj`` and
+        ``attn_fused_o`` the launch also adds the o-projection into resid;
+        returns whether it did."""
         B, Hq, Hkv, C, s = self.batch, self.HEADS, self.KV_HEADS, self.capacity, self._s
         pos, attn = _ptr(self.g_pos), _ptr(self.attn_out)
         common = (_ptr(L["q_norm"]), _ptr(L["k_norm"]), _ptr(self.cos_table), _ptr(self.sin_table), pos, kc, vc)
+        if o_proj and self.attn_fused_o:
+            call("q3_attn_decode_fused_o", *src, *common, _ptr(self.attn_x), attn, _ptr(L["o"]), self.HIDDEN,
+                 _ptr(self.resid), _ptr(self.attn_xo), B, Hq, Hkv, C, self.splits, i, self.EPS, self.SCALE,
+                 _ptr(self.attn_err), s)
+            return True
         if self.attn_fused:
             call("q3_attn_decode_fused", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i,
                  self.EPS, self.SCALE, _ptr(self.attn_err), s)
-            return
+            return False
         call("q3_attn_decode", *src, *common, _ptr(self.part_acc), _ptr(self.part_ml),
              attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
         if self.splits > 1:
             call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
+        return False
 
     def _proj(self, x: int, ldx: int, w: torch.Tensor, N: int, K: int, epi: int, y: int, ldy: int) -> None:
         """Decode projection for batches outside the GEMV and fused MFMA paths (more
@@ -517,6 +538,7 @@ class Engine:
         decode stream.  Its flags are derived from (position, layer), so words
         left by an earlier call at the same positions would read as fresh."""
         self.attn_x.zero_()
+        self.attn_xo.zero_()
         self.attn_err.zero_()
 
     def _begin_decode(self, logits: torch.Tensor, seq_len: int) -> None:
@@ -540,8 +562,8 @@ class Engine:
         if self.attn_fused:
             if int(self.attn_err.cpu()[0]):
                 self.graph_key_reset()
-                raise RuntimeError("q3_attn_decode_fused did not complete: a merge workgroup waited "
-                                   "past its time bound")
+                raise RuntimeError("the fused attention launch did not complete: a merge or o-projection "
+                                   "workgroup waited past its time bound")
             return
         if not self.persist:
             return
@@ -682,6 +704,7 @@ class Engine:
         logits = self._forward_prefill(ids, seq_len)
         self._begin_decode(logits, seq_len)
         host = torch.empty(batch, dtype=torch.int64, pin_memory=True)
+        host_err = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         done = torch.cuda.Event()
         pending = False
         for step in range(max_new_tokens):
@@ -691,6 +714,8 @@ class Engine:
             else:
                 done.synchronize()
                 out = host.clone()
+                if self.attn_fused and int(host_err[0]):
+                    self._check_step()  # raises
             toks = out.tolist()
             if self.persist:
                 self._check_step(toks)
@@ -698,6 +723,7 @@ class Engine:
                 self._decode_step()
                 with torch.cuda.stream(self.stream):
                     host.copy_(self.g_token, non_blocking=True)
+                    host_err.copy_(self.attn_err, non_blocking=True)
                     done.record(self.stream)
                 pending = True
             else:

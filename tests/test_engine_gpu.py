@@ -137,23 +137,25 @@ def test_fused_mfma_decode_matches_oracle(tile_engine, tile_ckpt, batch):
     assert list(tile_engine.generate(ids, 6)) == steps
 
 
-def _trace_attention(engine, ids, n, fused):
-    saved = engine_mod.FUSED_ATTENTION
-    engine_mod.FUSED_ATTENTION = fused
+def _trace_attention(engine, ids, n, fused, fused_o=False):
+    saved = engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION
+    engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION = fused, fused_o
     try:
         steps, logits = engine.trace_logits(ids, n)
         assert engine.attn_fused == fused
+        assert engine.attn_fused_o == (fused and fused_o and len(ids) == 1)
         tokens = list(engine.generate(ids, n))
         assert int(engine.attn_err.cpu()[0]) == 0
     finally:
-        engine_mod.FUSED_ATTENTION = saved
+        engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION = saved
     return steps, logits, tokens
 
 
 @pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700), (4, 260), (5, 300)])
 def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, batch, prompt):
-    """Contexts long enough for split attention (2..16 splits, grid within one
-    wave of workgroups) run attention and its split merge as one launch.  Same
+    """Contexts long enough for split attention (2..16 splits, grid resident at
+    once) run attention and its split merge as one launch (at batch 1, opt-in,
+    with the o-projection as well).  Same
     bits as the two-launch path at every step, for trace_logits and generate,
     across repeated calls (the exchange words are cleared per call), and the
     oracle's stream.  Batch 5 takes the MFMA (tiled-weight) step."""
@@ -164,6 +166,9 @@ def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, bat
     s_steps, s_logits, s_tokens = _trace_attention(tile_engine, ids, 8, False)
     assert torch.equal(f_logits, s_logits)
     assert f_steps == s_steps == f_tokens == s_tokens
+    if batch == 1:  # the opt-in o-projection in the same launch: the same bits again
+        o_steps, o_logits, o_tokens = _trace_attention(tile_engine, ids, 8, True, fused_o=True)
+        assert torch.equal(o_logits, s_logits) and o_steps == s_steps == o_tokens
     orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
     want, want_logits = orc.generate(ids, 8, keep_logits=True)
     check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)

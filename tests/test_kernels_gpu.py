@@ -628,6 +628,56 @@ def test_attn_decode_fused(B, C, pos, splits, qsplits):
     assert err.item() == 0
 
 
+@pytest.mark.parametrize("Hq,Hkv,N,C,pos,splits", [(32, 8, 2560, 1536, 1100, 12), (32, 8, 2560, 300, 0, 2),
+                                                    (32, 8, 2560, 2000, 1999, 16), (8, 2, 512, 700, 650, 6),
+                                                    (16, 4, 1000, 900, 500, 5)])
+def test_attn_decode_fused_o(Hq, Hkv, N, C, pos, splits):
+    """Attention + merge + o-projection (residual join) in one launch ==
+    q3_attn_decode_fused then q3_gemv(X_PLAIN, EPI_RESID), bit for bit: the
+    attention output, the cache append and the residual, over several layers'
+    flags and a repeated (position, layer) after zeroing the exchange words.
+    N = 1000 leaves the last wave's second row past the end."""
+    B, D = 1, 128
+    width = (Hq + 2 * Hkv) * D
+    grid = call("q3_attn_fused_o_grid", B, Hq, Hkv, C, splits, N)
+    assert grid == call("q3_attn_fused_grid", B, Hq, Hkv, C, splits) + (N + 7) // 8
+    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    ow = dv(rnd((N, Hq * D), 0.02, 6))
+    posd = dv(torch.tensor([pos]))
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
+    xo = torch.zeros(call("q3_attn_xo_words", Hq), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for layer, seed in ((0, 7), (1, 8), (0, 9)):
+        if layer == 0 and seed == 9:
+            xbuf.zero_()
+            xo.zero_()
+        src = (P(dv(rnd((B, width), 1.5, seed))), width, None, 0)
+        res0 = rnd((B, N), 1.0, seed + 20)
+        got = []
+        for fused in (False, True):
+            ckd, cvd, res = dv(ck), dv(cv), dv(res0)
+            out = dv(torch.empty(B, Hq * D, dtype=torch.bfloat16))
+            common = (P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd), P(ckd), P(cvd), P(xbuf), P(out))
+            if fused:
+                call("q3_attn_decode_fused_o", *src, *common, P(ow), N, P(res), P(xo), B, Hq, Hkv, C, splits,
+                     layer, 1e-6, D ** -0.5, P(err), S())
+            else:
+                call("q3_attn_decode_fused", *src, *common, B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5,
+                     P(err), S())
+                call("q3_gemv", _lib.X_PLAIN, P(out), Hq * D, None, None, 0.0, None, P(ow), B, N, Hq * D,
+                     _lib.EPI_RESID, P(res), N, None, None, None, None, None, S())
+            torch.cuda.synchronize()
+            got.append((out.cpu(), res.cpu(), ckd.cpu(), cvd.cpu()))
+        for a, b in zip(*got):
+            assert torch.equal(a, b), (layer, seed)
+        assert not torch.equal(got[1][1], res0)
+    assert err.item() == 0
+    assert call("q3_attn_fused_o_grid", 2, Hq, Hkv, C, splits, N) == 0  # one sequence only
+
+
 @pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6)])
 def test_attn_decode_qkv_partials(B, C, pos, qsplits):
     """q/k/v from FP32 split partials == from their in-order sum rounded to BF16, bit for bit."""
