@@ -589,12 +589,12 @@ class Engine:
                 "a": self._empty(rows, self.q_size),
                 "act": self._empty(rows, self.INTER),
             }
-            if PREFILL_BLASLT:
-                bufs["t"] = self._empty(rows, self.HIDDEN)
-                bufs["gu"] = self._empty(rows, 2 * self.INTER)
-                if self.lt_ws is None:
-                    self.lt_ws = torch.empty(LT_WORKSPACE_BYTES, dtype=torch.uint8, device=self.device)
             self._prefill_bufs[rows] = bufs
+        if PREFILL_BLASLT and "gu" not in bufs:
+            bufs["t"] = self._empty(rows, self.HIDDEN)
+            bufs["gu"] = self._empty(rows, 2 * self.INTER)
+            if self.lt_ws is None:
+                self.lt_ws = torch.empty(LT_WORKSPACE_BYTES, dtype=torch.uint8, device=self.device)
         return bufs
 
     def _gemm_lt(self, x: int, ldx: int, w: torch.Tensor, M: int, N: int, K: int, y: int, ldy: int) -> None:
@@ -634,7 +634,7 @@ class Engine:
                 bufs = self._prefill_buffers(B * min(chunk, seq_len))
                 chunk_ids = ids[:, start:stop].contiguous()
                 resid, n, qkv, q, a, act = (_ptr(bufs[k]) for k in ("resid", "n", "qkv", "q", "a", "act"))
-                lt = "gu" in bufs
+                lt = PREFILL_BLASLT
                 for i, L in enumerate(self.layers):
                     if i == 0:
                         call("q3_embed_rmsnorm", _ptr(chunk_ids), _ptr(self.embed), resid, n,

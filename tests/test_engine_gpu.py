@@ -97,6 +97,29 @@ def test_prefill_logit_delta(tiny_engine):
     assert delta < min(TOL_TINY, 0.05 * max(np.abs(want).max(), 1.0)), delta
 
 
+def test_prefill_paths_agree(tiny_engine):
+    """The prompt pass with hipBLASLt projections (default) and with the library's
+    own MFMA GEMM and fused epilogues: both within TOL of HF's prefill logits and
+    of each other (they differ only in the projections' summation order)."""
+    g = golden("tiny_bf16")
+    ids = torch.from_numpy(g["prefill/ids"])
+    want = g["prefill/logits"]
+    saved = engine_mod.PREFILL_BLASLT
+    outs = []
+    try:
+        for lt in (True, False, True):
+            engine_mod.PREFILL_BLASLT = lt
+            tiny_engine._ensure_shape(2, 40, 4)
+            outs.append(tiny_engine._forward_prefill(ids, 40).float().cpu()[:, 0])
+            tiny_engine.stream.synchronize()
+    finally:
+        engine_mod.PREFILL_BLASLT = saved
+    for o in outs:
+        assert np.abs(o.numpy() - want).max() < TOL_TINY
+    assert (outs[0] - outs[1]).abs().max() <= TOL_TINY
+    assert torch.equal(outs[0], outs[2])  # each path is deterministic, and switching back restores it
+
+
 def test_yield_contract(tiny_engine):
     out = list(tiny_engine.generate([[1, 2, 3]], 1))
     assert len(out) == 1 and len(out[0]) == 1
