@@ -45,21 +45,33 @@ extern "C" {
 
 const char *q3_error_string(int code);
 
+/* ---- step records of the greedy loop ---------------------------------------
+ * A decode step's input token sits at position p = *pos; its logits predict
+ * position q = p + 1.  Two optional device tables, indexed by q, let the
+ * captured step replay a given token stream (teacher forcing) and record what
+ * it computed, with no host copy per step:
+ *   feed [npos, B] int64: the token fed at q, or -1 for the greedy choice;
+ *   rec  [npos, B, 4] int32: {argmax, max logit, logit of the token fed at q,
+ *        token fed at q}; logits as the FP32 bits of the BF16 value.
+ * The LM-head argmax epilogues (q3_gemv, q3_skinny_argmax) write the fed
+ * token's logit; q3_argmax_finish / q3_argmax_rows write the rest and feed the
+ * next step.  The contest judge's replay (QWEN_ENGINE_CONTRACT.md "The
+ * quality rule") needs exactly these two logits per position. */
+
 /* Decode projection for M <= 8 rows: y = epi(x' . W^T), x' per x_mode.
  * Replaces _linear (engine.py:431) fused with the input norm (engine.py:790,
  * fused.py:115 add_norm) and the residual / SwiGLU / argmax that follow it.
  * W is [N, K]; K % 8 == 0; x, W 16-byte aligned; ldx % 8 == 0.  Modes:
  * X_EMBED_NORM with EPI_STORE; X_PLAIN with EPI_STORE or EPI_RESID; X_NORM
- * with any epilogue.  EPI_SWIGLU (N % 4 == 0) writes N/2 columns.  EPI_ARGMAX writes part_val/part_idx
- * [q3_gemv_partials(M, N, epi), M]; with tokens != NULL the last workgroup
- * also reduces them into tokens[M] (int64), advances *pos when pos != NULL,
- * and resets *counter (a device int, zero before the first call); otherwise
- * finish with q3_argmax_finish. */
+ * with any epilogue.  EPI_SWIGLU (N % 4 == 0) writes N/2 columns.  EPI_ARGMAX
+ * writes part_val/part_idx [q3_gemv_partials(M, N, epi), M] for
+ * q3_argmax_finish; with rec != NULL (argmax epilogues only; pos and feed then
+ * required) it also writes the fed token's logit into the step record. */
 int q3_gemv(int x_mode, const uint16_t *x, int ldx, const int64_t *ids,
             const uint16_t *norm_w, float eps, uint16_t *resid_out,
             const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, float *part_val, int *part_idx,
-            int64_t *tokens, int64_t *pos, int *counter, hipStream_t stream);
+            const int64_t *pos, const int64_t *feed, int32_t *rec, int npos, hipStream_t stream);
 int q3_gemv_partials(int M, int N, int epi);
 
 /* Dense projection for any M (MFMA, LDS-tiled): y = epi(x . W^T), epi in
@@ -106,6 +118,7 @@ int q3_skinny_partials(const uint16_t *x, int ldx, const uint16_t *wt, int M, in
  * logits [M, ld_logits] are stored too when non-NULL.  engine/engine.py:833. */
 int q3_skinny_argmax(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
                      uint16_t *logits, int ld_logits, float *part_val, int *part_idx,
+                     const int64_t *pos, const int64_t *feed, int32_t *rec, int npos,
                      hipStream_t stream);
 /* Repack row-major W [N, K] (N % 16 == 0, K % 32 == 0) into 16-row tiles:
  * element (n, k) goes to ((n/16 * K/32 + k/32) * 64 + (k%32)/8 * 16 + n%16) * 8
@@ -195,26 +208,6 @@ int q3_attn_decode_fused(const uint16_t *qkv, int ld_qkv, const float *qkv_part,
 int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits);
 int q3_attn_xbuf_words(int B, int Hq, int splits);
 
-/* The fused launch of one sequence (B = 1) plus the o-projection that follows
- * it: resid[r] = bf16(resid[r] + bf16(attn . o_w[r])) for r < N (o_w [N, Hq*128],
- * Hq*128 <= 4096 and a multiple of 512).  Its workgroups load o_w while the
- * attention runs and read the merged heads as flagged words from xo
- * (q3_attn_xo_words(Hq) words, 16-byte aligned, zeroed at the start of every
- * call like xbuf).  Bit-identical to q3_attn_decode_fused followed by
- * q3_gemv(X_PLAIN, o_w, EPI_RESID).  Replaces decode_attention + the o_proj
- * _linear with its add_norm residual (engine.py:720-732,450-456).
- * q3_attn_fused_o_grid returns the grid, or 0 where this launch does not
- * apply (B != 1, no fused grid, or not resident at once). */
-int q3_attn_decode_fused_o(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
-                           const uint16_t *q_norm_w, const uint16_t *k_norm_w,
-                           const uint16_t *cos_table, const uint16_t *sin_table, const int64_t *pos,
-                           uint16_t *cache_k, uint16_t *cache_v, uint32_t *xbuf, uint16_t *out,
-                           const uint16_t *o_w, int N, uint16_t *resid, uint32_t *xo, int B, int Hq,
-                           int Hkv, int capacity, int splits, int layer, float eps, float scale,
-                           int *err, hipStream_t stream);
-int q3_attn_fused_o_grid(int B, int Hq, int Hkv, int capacity, int splits, int N);
-int q3_attn_xo_words(int Hq);
-
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
  * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /
  * chunk mask (engine.py:263-280,777-787). */
@@ -222,60 +215,21 @@ int q3_attn_prefill(const uint16_t *q, const uint16_t *cache_k, const uint16_t *
                     uint16_t *out, int B, int T, int start, int Hq, int Hkv,
                     int capacity, float scale, hipStream_t stream);
 
-/* Greedy token from the argmax partials (first index on ties): tokens[b]
- * (int64); when pos != NULL, *pos += 1 (the self-feeding graph's advance,
- * engine.py:833-838). */
+/* Greedy token from the argmax partials (first index on ties), for each of the
+ * B rows: tokens[b] (int64) = the token fed next, i.e. feed[q][b] when feed is
+ * given and that entry is >= 0, else the argmax; rec[q][b] is filled when
+ * given (the step records above; npos positions).  When pos != NULL, *pos
+ * advances by one (the self-feeding graph's advance, engine.py:833-838): every
+ * block reads it first and the last block to finish advances it, through
+ * *counter (a device int, zero before the first call; not needed for B == 1). */
 int q3_argmax_finish(const float *part_val, const int *part_idx, int nparts, int B,
-                     int64_t *tokens, int64_t *pos, hipStream_t stream);
-/* Argmax over stored BF16 logits rows [B, V] (first index on ties); when
- * pos != NULL, *pos += 1. */
+                     int64_t *tokens, int64_t *pos, int *counter, const int64_t *feed,
+                     int32_t *rec, int npos, hipStream_t stream);
+/* The same over stored BF16 logits rows [B, V] (first index on ties); the fed
+ * token's logit is read from the row. */
 int q3_argmax_rows(const uint16_t *logits, int ld, int B, int V, int64_t *tokens,
-                   int64_t *pos, hipStream_t stream);
-
-/* ---- whole-step persistent decode, one sequence ------------------------------ */
-
-/* One layer's device pointers (BF16 [N, K] row-major weights and gains), as the
- * persistent kernel reads them from a device array of L entries. */
-typedef struct q3_layer {
-    const uint16_t *qkv;     /* [(Hq + 2 Hkv) * 128, H]: q | k | v rows          */
-    const uint16_t *o;       /* [H, Hq * 128]                                     */
-    const uint16_t *gate_up; /* [2 I, H], rows (gate_j, up_j) interleaved         */
-    const uint16_t *down;    /* [H, I]                                            */
-    const uint16_t *in_ln, *post_ln, *q_norm, *k_norm; /* [H], [H], [128], [128]  */
-} q3_layer;
-
-/* The whole self-feeding decode step of one sequence (B = 1) in one launch of
- * `grid` workgroups (q3_persist_grid(): one per CU, all resident): embedding,
- * L x (RMSNorm, qkv, q/k RMSNorm + RoPE + KV append, split attention + merge,
- * o + residual, RMSNorm, gate/up + SwiGLU, down + residual), final RMSNorm, LM
- * head, greedy argmax into tokens[0], *pos += 1.  Replaces the captured
- * _forward_decode step (engine.py:805-839) as one kernel instead of one per op.
- * cache_k/v [L, 1, Hkv, capacity, 128]; cos/sin [>= capacity, 128]; logits
- * [V] BF16 stored when non-NULL.  work: q3_persist_work_bytes() bytes, 256-byte
- * aligned, zeroed once before the first call and then owned by this entry point
- * (it carries a step epoch between calls; re-zero it after an error).  Shapes:
- * H, I, Hq*128 multiples of 512, H <= 4096, I <= 16384, Hq == 4 Hkv, and
- * q3_persist_supported() true.  A launch that cannot complete (a workgroup not
- * resident, a wait past 1 s) writes tokens[0] = -1 and exits.  trace: NULL,
- * or q3_persist_trace_words(L) words of timestamps (below). */
-int q3_persist_grid(void);
-int q3_persist_supported(int L, int H, int I, int V, int Hq, int Hkv, int capacity, int grid);
-int64_t q3_persist_work_bytes(int H, int I, int Hq, int Hkv, int grid);
-int q3_decode_persistent(const q3_layer *layers, int L, const uint16_t *embed, const uint16_t *final_norm,
-                         const uint16_t *lm_head, int H, int I, int V, int Hq, int Hkv,
-                         const uint16_t *cos_t, const uint16_t *sin_t, uint16_t *cache_k, uint16_t *cache_v,
-                         int capacity, int64_t *tokens, int64_t *pos, void *work, int grid, uint16_t *logits,
-                         float eps, float scale, uint64_t *trace, hipStream_t stream);
-/* Words of the optional step trace of q3_decode_persistent (trace != NULL):
- * for workgroups 0, 1, grid/2 and grid-1, per layer 16 wall-clock (100 MHz)
- * stamps of the control wave's phase boundaries, then two stamps per streamed
- * matrix from compute wave 0 (began waiting for the input, saw it), then one
- * per streamed matrix from loader wave 0 (issued its first unit); then, for
- * every workgroup and layer, [L][grid][8] words (qkv done, attention inputs
- * ready, attention done, merge done, merge poll start, merge polls, loader 0's
- * polls of a full ring, compute wave 0's polls for landed units).  A
- * diagnostic: steps run slower while tracing. */
-int q3_persist_trace_words(int L, int grid);
+                   int64_t *pos, int *counter, const int64_t *feed, int32_t *rec, int npos,
+                   hipStream_t stream);
 
 /* hipGraph capture of everything enqueued on `stream` between begin and end
  * (engine.py:1029-1065). */

@@ -176,6 +176,9 @@ class Qwen3Oracle:
             })
         self.cos = self.sin = None
         self.cache_k = self.cache_v = None
+        #: The projection; tests swap in another summation order (see
+        #: ``f32_linear``) to measure what reordering alone moves.
+        self.linear = linear
 
     def reset(self, batch: int, capacity: int) -> None:
         """Fresh cache of ``capacity`` slots (reference ``engine/engine.py:843-862``)."""
@@ -194,9 +197,10 @@ class Qwen3Oracle:
 
         residual = x
         h = rms_norm(x, L["in_ln"], self.eps)
-        q = rms_norm(linear(h, L["q"]).view(B, T, self.Hq, self.D), L["q_norm"], self.eps)
-        k = rms_norm(linear(h, L["k"]).view(B, T, self.Hkv, self.D), L["k_norm"], self.eps)
-        v = linear(h, L["v"]).view(B, T, self.Hkv, self.D)
+        lin = self.linear
+        q = rms_norm(lin(h, L["q"]).view(B, T, self.Hq, self.D), L["q_norm"], self.eps)
+        k = rms_norm(lin(h, L["k"]).view(B, T, self.Hkv, self.D), L["k_norm"], self.eps)
+        v = lin(h, L["v"]).view(B, T, self.Hkv, self.D)
         q = apply_rope(q.transpose(1, 2), cos, sin)
         k = apply_rope(k.transpose(1, 2), cos, sin)
         self.cache_k[i][:, :, start:start + T] = k
@@ -204,11 +208,11 @@ class Qwen3Oracle:
         a = attention(q, self.cache_k[i][:, :, :start + T], self.cache_v[i][:, :, :start + T],
                       self.scale, start)
         a = a.transpose(1, 2).reshape(B, T, self.Hq * self.D)
-        x = residual + linear(a, L["o"])
+        x = residual + lin(a, L["o"])
 
         residual = x
         h = rms_norm(x, L["post_ln"], self.eps)
-        mlp = linear(swiglu(linear(h, L["gate"]), linear(h, L["up"])), L["down"])
+        mlp = lin(swiglu(lin(h, L["gate"]), lin(h, L["up"])), L["down"])
         return residual + mlp
 
     @torch.inference_mode()
@@ -218,7 +222,7 @@ class Qwen3Oracle:
         for i in range(len(self.layers)):
             x = self.block(x, i, start)
         x = rms_norm(x, self.final_norm, self.eps)
-        return linear(x[:, -1, :], self.lm_head)
+        return self.linear(x[:, -1, :], self.lm_head)
 
     @torch.inference_mode()
     def prefill(self, ids: torch.Tensor, chunk: int | None = None) -> torch.Tensor:
@@ -253,6 +257,23 @@ class Qwen3Oracle:
             if step + 1 < max_new_tokens:
                 logits = self.forward(token.view(B, 1), P + step)
         return steps, kept
+
+
+class f32_linear:
+    """``x @ W.T`` summed by torch's FP32 GEMM (weights kept as FP32 copies),
+    rounded once to BF16: the same products and one rounding as ``linear``, in
+    another summation order -- a reordering the reference accepts
+    (``AGENTS.md`` "reorder freely, never reformulate").  Used only to
+    measure the logit noise that reordering alone produces."""
+
+    def __init__(self):
+        self.w32 = {}
+
+    def __call__(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        w = self.w32.get(id(weight))
+        if w is None:
+            w = self.w32[id(weight)] = weight.float()
+        return (x.float() @ w.T).to(x.dtype)
 
 
 def top2_gap(logits: torch.Tensor) -> torch.Tensor:

@@ -28,7 +28,7 @@ _Z = ctypes.c_size_t
 #: name -> argtypes (restype int unless listed in _RESTYPES)
 SIGNATURES = {
     "q3_error_string": [_I],
-    "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P],
+    "q3_gemv": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _I, _P],
     "q3_gemv_partials": [_I, _I, _I],
     "q3_gemm": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P],
     "q3_gemm_lt": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _Z, _P],
@@ -36,7 +36,7 @@ SIGNATURES = {
     "q3_skinny": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_tiled": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_partials": [_P, _I, _P, _I, _I, _I, _P, _P],
-    "q3_skinny_argmax": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _P],
+    "q3_skinny_argmax": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _I, _P],
     "q3_tile16": [_P, _I, _I, _P, _P],
     "q3_skinny_splits": [_I, _I, _I],
     "q3_skinny_ws_floats": [_I, _I, _I],
@@ -51,32 +51,20 @@ SIGNATURES = {
     "q3_attn_decode_fused": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F,
                              _P, _P],
     "q3_attn_fused_grid": [_I, _I, _I, _I, _I],
-    "q3_attn_decode_fused_o": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
-                               _I, _F, _F, _P, _P],
-    "q3_attn_fused_o_grid": [_I, _I, _I, _I, _I, _I],
-    "q3_attn_xo_words": [_I],
     "q3_attn_xbuf_words": [_I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
-    "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P],
-    "q3_argmax_rows": [_P, _I, _I, _I, _P, _P, _P],
-    "q3_persist_grid": [],
-    "q3_persist_supported": [_I, _I, _I, _I, _I, _I, _I, _I],
-    "q3_persist_work_bytes": [_I, _I, _I, _I, _I],
-    "q3_decode_persistent": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P,
-                             _F, _F, _P, _P],
-    "q3_persist_trace_words": [_I, _I],
+    "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P],
+    "q3_argmax_rows": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P],
     "q3_graph_begin": [_P],
     "q3_graph_end": [_P, ctypes.POINTER(ctypes.c_void_p)],
     "q3_graph_launch": [_P, _P],
     "q3_graph_destroy": [_P],
 }
-_RESTYPES = {"q3_error_string": ctypes.c_char_p, "q3_persist_work_bytes": ctypes.c_int64}
+_RESTYPES = {"q3_error_string": ctypes.c_char_p}
 
 #: entry points that return a count, not an error code
 _COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words",
-           "q3_attn_fused_o_grid", "q3_attn_xo_words",
-           "q3_skinny_splits", "q3_skinny_ws_floats",
-           "q3_persist_grid", "q3_persist_supported", "q3_persist_work_bytes", "q3_persist_trace_words"}
+           "q3_skinny_splits", "q3_skinny_ws_floats"}
 
 _LIB: ctypes.CDLL | None = None
 

@@ -394,88 +394,6 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
     attn_unit<WAVES, QP>(a, blockIdx.x, blockIdx.y, blockIdx.z, nullptr, 0);
 }
 
-// The o-projection of one sequence inside the fused launch: y = resid +=
-// bf16(attn . W_o^T), W_o [N, K] with K = Hq * 128 <= 4096 (K % 512 == 0).
-// Each wave owns OROWS consecutive rows; it issues every weight load at
-// entry, while attention and the merge are still running, then the
-// workgroup polls the merged heads (flagged words from the merge role) into
-// LDS.  Per row: the q3_gemv order exactly (lane l sums chunks l*8 + 512u,
-// u ascending, with v_dot2; then the wave sum; then bf16(r + bf16(acc))), so
-// the result is bit-identical to attention followed by that GEMV.
-struct OProj {
-    const bf16_t* w = nullptr;  // null: no o-projection role
-    bf16_t* resid = nullptr;
-    uint32_t* xo = nullptr;     // Hq * 128 flagged words, zeroed at the start of every call
-    int N = 0;
-};
-constexpr int OROWS = 2;
-constexpr int OMAXK = 4096;
-
-__device__ void o_role(const DecodeArgs& a, const OProj& o, uint32_t F, int oi, int* err) {
-    __shared__ __align__(16) bf16_t ox[OMAXK];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int K = a.Hq * D, KU = K / 512;
-    const int row0 = (oi * 4 + w) * OROWS;
-    u32x4_t wv[OROWS][OMAXK / 512];
-#pragma unroll
-    for (int k = 0; k < OROWS; ++k) {
-        const bf16_t* wr = o.w + (int64_t)min(row0 + k, o.N - 1) * K + lane * 8;
-#pragma unroll
-        for (int u = 0; u < OMAXK / 512; ++u)  // chunks past K re-read the last one and are not used
-            wv[k][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + min(u, KU - 1) * 512));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    const auto rx = q3x::rsrc(o.xo);
-    const uint32_t Fs = F << 16;
-    q3x::SpinBound sb;
-    int timed_out = 0;
-    // A one-word probe first (cheap while attention runs), then every word.
-    for (;;) {
-        const uint32_t hint = __builtin_amdgcn_raw_buffer_load_b32(rx, (K - 1) * 4, 0, q3x::SC1);
-        if ((hint >> 16) == F) break;
-        __builtin_amdgcn_s_sleep(2);
-        if (!sb.ok(q3x::SPIN_LIMIT)) {
-            timed_out = 1;
-            break;
-        }
-    }
-    for (;;) {
-        uint32_t bad = 0;
-        for (int c = tid; c < K / 4; c += 256) {
-            const u32x4_t v = q3x::ld_coh(rx, c * 16);
-            bad |= q3x::unflagged(v, Fs);
-            *reinterpret_cast<uint2*>(ox + 4 * c) = make_uint2(q3x::bfpair(v.x, v.y), q3x::bfpair(v.z, v.w));
-        }
-        if (!sb.ok(q3x::SPIN_LIMIT)) timed_out = 1;
-        // Both decisions are made for the whole workgroup (barriers stay matched).
-        const int again = __syncthreads_or(bad != 0);
-        if (__syncthreads_or(timed_out)) {
-            timed_out = 1;
-            break;
-        }
-        if (!again) break;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    if (timed_out) {
-        if (err != nullptr && tid == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < OROWS; ++k) {
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < OMAXK / 512; ++u)
-            if (u < KU) {
-                const uint4 x = *reinterpret_cast<const uint4*>(ox + lane * 8 + u * 512);
-                const u32x4_t wk = wv[k][u];
-                acc = dot8(make_uint4(wk.x, wk.y, wk.z, wk.w), x, acc);
-            }
-        acc = wave_sum(acc);
-        const int r = row0 + k;
-        if (lane == 0 && r < o.N) o.resid[r] = (bf16_t)f2bf(bf2f(o.resid[r]) + rbf(acc));
-    }
-}
-
 // Attention and split merge in one launch (several splits, small grids).  The
 // first splits * Hkv * B workgroups are the attention units above (the wave
 // count q3_attn_decode would use, so the partials are the same bits); each
@@ -488,7 +406,7 @@ __device__ void o_role(const DecodeArgs& a, const OProj& o, uint32_t F, int oi, 
 // its wait is still bounded (1 s), after which it writes zeros and sets *err.
 template <int WAVES, int QP>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(DecodeArgs a, uint32_t* xbuf, int layer,
-                                                                          int* err, OProj o) {
+                                                                          int* err) {
     constexpr int HPW = WAVES / 2;  // heads per merging workgroup (128 threads each)
     const int n_att = a.splits * a.Hkv * a.B;
     const int n_mrg = a.Hq / HPW * a.B;
@@ -500,10 +418,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(Decod
         attn_unit<WAVES, QP>(a, split, kvh, b, xbuf, F);
         return;
     }
-    if (bid >= n_att + n_mrg) {
-        if constexpr (WAVES == 4) o_role(a, o, F, bid - n_att - n_mrg, err);
-        return;
-    }
+    if (bid >= n_att + n_mrg) return;
     // Merge: heads HPW mi .. HPW mi + HPW - 1 of sequence b; thread t takes
     // (head t / 128, d = t % 128).
     constexpr int CH = 16;
@@ -567,9 +482,6 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(Decod
     }
     const uint32_t y = f2bf(l_run > 0.f ? acc / l_run : 0.f);
     a.out[((int64_t)b * a.Hq + h) * D + d] = (bf16_t)y;
-    if (o.w != nullptr)
-        __builtin_amdgcn_raw_buffer_store_b32(q3x::word(y, F), q3x::rsrc(o.xo), ((b * a.Hq + h) * D + d) * 4, 0,
-                                              q3x::SC1);
 }
 
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
@@ -885,8 +797,7 @@ static int attn_fused_launch(const bf16_t* qkv, int ld_qkv, const float* qkv_par
                              const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
                              const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
                              uint32_t* xbuf, bf16_t* out, int B, int Hq, int Hkv, int capacity, int splits,
-                             int layer, float eps, float scale, int* err, const OProj& o, int grid,
-                             hipStream_t stream) {
+                             int layer, float eps, float scale, int* err, int grid, hipStream_t stream) {
     if (grid == 0 || Hq != GROUP * Hkv || capacity < 1 || layer < 0 || layer >= 64 ||
         ld_qkv < (Hq + 2 * Hkv) * D || (!qkv && !qkv_part) ||
         (qkv_part && (qkv_splits < 1 || (reinterpret_cast<uintptr_t>(qkv_part) & 3))) || !pos || !cache_k ||
@@ -895,9 +806,9 @@ static int attn_fused_launch(const bf16_t* qkv, int ld_qkv, const float* qkv_par
     DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos,
                  cache_k, cache_v, nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B};
     const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
-    if (qp == 0) Q3_LAUNCH((attn_fused_kernel<4, 0>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err, o);
-    else if (qp == 1) Q3_LAUNCH((attn_fused_kernel<4, 1>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err, o);
-    else Q3_LAUNCH((attn_fused_kernel<4, 2>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err, o);
+    if (qp == 0) Q3_LAUNCH((attn_fused_kernel<4, 0>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
+    else if (qp == 1) Q3_LAUNCH((attn_fused_kernel<4, 1>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
+    else Q3_LAUNCH((attn_fused_kernel<4, 2>), dim3(grid), dim3(4 * 64), 0, stream, a, xbuf, layer, err);
     Q3_CHECK_LAUNCH();
 }
 
@@ -908,38 +819,7 @@ extern "C" int q3_attn_decode_fused(const bf16_t* qkv, int ld_qkv, const float* 
                                     int layer, float eps, float scale, int* err, hipStream_t stream) {
     return attn_fused_launch(qkv, ld_qkv, qkv_part, qkv_splits, q_norm_w, k_norm_w, cos_table, sin_table, pos,
                              cache_k, cache_v, xbuf, out, B, Hq, Hkv, capacity, splits, layer, eps, scale, err,
-                             OProj{}, q3_attn_fused_grid(B, Hq, Hkv, capacity, splits), stream);
-}
-
-// Grid of the fused launch with the o-projection role (one sequence), or 0.
-extern "C" int q3_attn_fused_o_grid(int B, int Hq, int Hkv, int capacity, int splits, int N) {
-    const int K = Hq * D;
-    if (B != 1 || N < 1 || K > OMAXK || K % 512) return 0;
-    const int base = q3_attn_fused_grid(B, Hq, Hkv, capacity, splits);
-    if (base == 0) return 0;
-    const long grid = base + (N + 4 * OROWS - 1) / (4 * OROWS);
-    return grid <= fused_resident() ? (int)grid : 0;
-}
-
-extern "C" int q3_attn_xo_words(int Hq) { return Hq * D; }
-
-extern "C" int q3_attn_decode_fused_o(const bf16_t* qkv, int ld_qkv, const float* qkv_part, int qkv_splits,
-                                      const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
-                                      const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k,
-                                      bf16_t* cache_v, uint32_t* xbuf, bf16_t* out, const bf16_t* o_w, int N,
-                                      bf16_t* resid, uint32_t* xo, int B, int Hq, int Hkv, int capacity,
-                                      int splits, int layer, float eps, float scale, int* err,
-                                      hipStream_t stream) {
-    if (!o_w || !resid || !xo || (reinterpret_cast<uintptr_t>(xo) & 15) || (reinterpret_cast<uintptr_t>(o_w) & 15))
-        return (int)hipErrorInvalidValue;
-    OProj o;
-    o.w = o_w;
-    o.resid = resid;
-    o.xo = xo;
-    o.N = N;
-    return attn_fused_launch(qkv, ld_qkv, qkv_part, qkv_splits, q_norm_w, k_norm_w, cos_table, sin_table, pos,
-                             cache_k, cache_v, xbuf, out, B, Hq, Hkv, capacity, splits, layer, eps, scale, err, o,
-                             q3_attn_fused_o_grid(B, Hq, Hkv, capacity, splits, N), stream);
+                             q3_attn_fused_grid(B, Hq, Hkv, capacity, splits), stream);
 }
 
 extern "C" int q3_attn_merge(const float* part_acc, const float* part_ml, bf16_t* out, int B, int Hq,

@@ -116,6 +116,20 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
 // then one rounding (reference fused.py:107-111).
 __device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + expf(-g))); }
 
+// Step records of the greedy loop, indexed by the position q a step's logits
+// predict (q = *pos + 1 for the step whose input sits at *pos):
+//   feed [npos, B] int64: the token fed at q, or < 0 for the greedy choice;
+//   rec  [npos, B, 4] int32: {argmax, max logit (FP32 bits of the BF16 value),
+//        logit of the token fed at q (same encoding), token fed at q}.
+// The LM-head epilogues write the fed token's logit; the argmax finish writes
+// the rest and feeds the next step.
+struct StepRec {
+    const int64_t* feed = nullptr;
+    int* rec = nullptr;
+    int npos = 0;
+};
+constexpr int REC_WORDS = 4;
+
 // hipGetLastError reports the last error of any runtime call on this thread,
 // so each launch first clears it: the check after the launch then reports
 // that launch, not a stale code an unrelated (already handled) call left.

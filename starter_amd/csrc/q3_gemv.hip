@@ -23,10 +23,10 @@
 //                          (fused.py:135-138);
 //             EPI_SWIGLU   weight rows interleaved (gate_j, up_j);
 //                          out[j] = bf16(bf16(silu(g)) * u) (fused.py:107-111);
-//             EPI_ARGMAX   per-workgroup (max bf16 logit, lowest index) partials;
-//                          with tokens != NULL the last workgroup to finish
-//                          (device-scope counter) reduces them, writes the
-//                          greedy tokens and advances *pos (engine.py:833-838).
+//             EPI_ARGMAX   per-workgroup (max bf16 logit, lowest index) partials
+//                          for q3_argmax_finish (engine.py:833-838), and the
+//                          logit of the token fed at *pos + 1 into the step
+//                          record when one is given.
 #include "q3_common.hpp"
 #include "q3.h"
 
@@ -49,9 +49,8 @@ struct GemvArgs {
     int ldy;
     float* part_val;      // EPI_ARGMAX: [gridDim.x, M]
     int* part_idx;
-    int64_t* tokens;      // fused argmax finish (optional)
-    int64_t* pos;
-    int* counter;
+    const int64_t* pos;   // argmax epilogues with a step record: this step's input position
+    StepRec sr;
 };
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
@@ -277,13 +276,13 @@ __device__ __forceinline__ void store_outputs(const GemvArgs& a, const float (&a
     }
 }
 
-// Argmax partials of this workgroup, and the fused finish in the last one.
+// Argmax partials of this workgroup; with a step record, the logit of the
+// token fed at *pos + 1 (from the wave that owns that row).
 template <int M, int R>
 __device__ void argmax_epilogue(const GemvArgs& a, const float (&acc)[R][M], int row0, bool active,
                                 int lane, int wave) {
     __shared__ float bval[GEMV_WAVES][M];
     __shared__ int bidx[GEMV_WAVES][M];
-    __shared__ int s_last;
     if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -299,6 +298,18 @@ __device__ void argmax_epilogue(const GemvArgs& a, const float (&acc)[R][M], int
             bval[wave][m] = best;
             bidx[wave][m] = bi;
         }
+        if (a.sr.rec != nullptr && active) {
+            const int64_t q = *a.pos + 1;
+            if (q >= 0 && q < a.sr.npos) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const int64_t t = a.sr.feed[q * M + m];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        if (row0 + r == t) a.sr.rec[(q * M + m) * REC_WORDS + 2] = __float_as_int(rbf(acc[r][m]));
+                }
+            }
+        }
     }
     __syncthreads();
     if (threadIdx.x < M) {
@@ -310,52 +321,6 @@ __device__ void argmax_epilogue(const GemvArgs& a, const float (&acc)[R][M], int
             if (better(bval[w][m], bidx[w][m], best, bi)) { best = bval[w][m]; bi = bidx[w][m]; }
         a.part_val[blockIdx.x * M + m] = best;
         a.part_idx[blockIdx.x * M + m] = bi;
-    }
-    if (a.tokens == nullptr) return;
-    // The last workgroup to arrive reduces every partial; the others just exit
-    // (nothing waits on anything, so no workgroup can stall the grid).
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const int prev = atomicAdd(a.counter, 1);
-        s_last = (prev == (int)gridDim.x - 1);
-        __threadfence();
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int nparts = gridDim.x;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int p = threadIdx.x; p < nparts; p += GEMV_THREADS) {
-            const float v = __builtin_nontemporal_load(a.part_val + p * M + m);
-            const int i = __builtin_nontemporal_load(a.part_idx + p * M + m);
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float v = __shfl_xor(bv, o, Q3_WAVE);
-            const int i = __shfl_xor(bi, o, Q3_WAVE);
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
-        __syncthreads();
-        if (lane == 0) { bval[wave][m] = bv; bidx[wave][m] = bi; }
-    }
-    __syncthreads();
-    if (threadIdx.x < M) {
-        const int m = threadIdx.x;
-        float bv = bval[0][m];
-        int bi = bidx[0][m];
-#pragma unroll
-        for (int w = 1; w < GEMV_WAVES; ++w)
-            if (better(bval[w][m], bidx[w][m], bv, bi)) { bv = bval[w][m]; bi = bidx[w][m]; }
-        a.tokens[m] = bi;
-    }
-    if (threadIdx.x == 0) {
-        if (a.pos) *a.pos += 1;
-        *a.counter = 0;  // ready for the next launch (kernel boundaries order it)
     }
 }
 
@@ -550,7 +515,7 @@ extern "C" int q3_gemv(int x_mode, const bf16_t* x, int ldx, const int64_t* ids,
                        const bf16_t* norm_w, float eps, bf16_t* resid_out,
                        const bf16_t* w, int M, int N, int K,
                        int epi, bf16_t* y, int ldy, float* part_val, int* part_idx,
-                       int64_t* tokens, int64_t* pos, int* counter, hipStream_t stream) {
+                       const int64_t* pos, const int64_t* feed, int* rec, int npos, hipStream_t stream) {
     if (M < 1 || M > Q3_GEMV_MAX_M || N < 1 || K < 8 || (K % 8) != 0) return (int)hipErrorInvalidValue;
     // Staged rows live in LDS (M*K BF16, within the 64 KiB default).
     if (x_mode != Q3_X_PLAIN && (K > Q3_GEMV_MAX_NORM_K || (size_t)M * K * 2 > LDS_X_LIMIT))
@@ -558,14 +523,18 @@ extern "C" int q3_gemv(int x_mode, const bf16_t* x, int ldx, const int64_t* ids,
     if (epi == Q3_EPI_SWIGLU && (N % 2) != 0) return (int)hipErrorInvalidValue;
     const bool argmax = epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX;
     if (argmax && (!part_val || !part_idx)) return (int)hipErrorInvalidValue;
-    if (argmax && tokens && !counter) return (int)hipErrorInvalidValue;
+    if (rec && (!argmax || !pos || !feed || npos < 1)) return (int)hipErrorInvalidValue;
     if (epi != Q3_EPI_ARGMAX && !y) return (int)hipErrorInvalidValue;
     if (x_mode == Q3_X_EMBED_NORM && (!ids || !resid_out)) return (int)hipErrorInvalidValue;
     if (x_mode != Q3_X_PLAIN && !norm_w) return (int)hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return (int)hipErrorInvalidValue;
     if (x_mode == Q3_X_PLAIN && (ldx % 8) != 0) return (int)hipErrorInvalidValue;
-    GemvArgs a{x, ldx, ids, norm_w, eps, resid_out, w, M, N, K, y, ldy, part_val, part_idx,
-               argmax ? tokens : nullptr, pos, counter};
+    GemvArgs a{x, ldx, ids, norm_w, eps, resid_out, w, M, N, K, y, ldy, part_val, part_idx, pos, StepRec{}};
+    if (rec) {
+        a.sr.feed = feed;
+        a.sr.rec = rec;
+        a.sr.npos = npos;
+    }
     int rc = -1;
     switch (x_mode) {
         case Q3_X_PLAIN: rc = dispatch_epi<Q3_X_PLAIN>(epi, a, stream); break;

@@ -242,15 +242,45 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-// grid (B), 1024 threads: reduce argmax partials [nparts, B] -> tokens[b];
-// block 0 advances *pos.  Each thread reads its partials four at a time with
-// the loads issued together; waves reduce with shuffles, then LDS.
+// The greedy choice (bv, bi) of row b for the step whose input sits at p:
+// tokens[b] = the token fed next (feed[p + 1] when set, else bi), the step
+// record of position p + 1, and the position advance.  Every block read p at
+// entry; the last of the B blocks to get here (a device counter; B == 1 needs
+// none) writes p + 1, so no block can read the advanced value.
+__device__ void finish_row(int b, int B, float bv, int bi, int64_t p, int64_t* tokens, int64_t* pos, int* counter,
+                           const StepRec& sr) {
+    const int64_t q = p + 1;
+    const bool inq = pos != nullptr && q >= 0 && q < sr.npos;
+    const int64_t f = (sr.feed != nullptr && inq) ? sr.feed[q * B + b] : -1;
+    const int64_t tok = f >= 0 ? f : bi;
+    tokens[b] = tok;
+    if (sr.rec != nullptr && inq) {
+        int* r = sr.rec + (q * B + b) * REC_WORDS;
+        r[0] = bi;
+        r[1] = __float_as_int(bv);
+        if (f < 0) r[2] = __float_as_int(bv);  // else the LM-head epilogue wrote it
+        r[3] = (int)tok;
+    }
+    if (pos == nullptr) return;
+    if (B == 1) {
+        *pos = q;
+    } else if (atomicAdd(counter, 1) == B - 1) {
+        *counter = 0;  // ready for the next launch (kernel boundaries order it)
+        *pos = q;
+    }
+}
+
+// grid (B), 1024 threads: reduce argmax partials [nparts, B] -> tokens[b]
+// (finish_row).  Each thread reads eight partials per round with the loads
+// issued together; waves reduce with shuffles, then LDS.
 constexpr int FIN_THREADS = 1024;
 __global__ __launch_bounds__(FIN_THREADS) void argmax_finish_kernel(const float* pv, const int* pi, int nparts,
-                                                                    int B, int64_t* tokens, int64_t* pos) {
+                                                                    int B, int64_t* tokens, int64_t* pos,
+                                                                    int* counter, StepRec sr) {
     __shared__ float sv[FIN_THREADS / 64];
     __shared__ int si[FIN_THREADS / 64];
     const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t p = pos != nullptr ? *pos : -2;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     // Eight partials per thread per round, all requested before any compare;
@@ -260,9 +290,9 @@ __global__ __launch_bounds__(FIN_THREADS) void argmax_finish_kernel(const float*
         int ix[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int p = min(p0 + j * FIN_THREADS, nparts - 1);
-            v[j] = pv[p * B + b];
-            ix[j] = pi[p * B + b];
+            const int pp = min(p0 + j * FIN_THREADS, nparts - 1);
+            v[j] = pv[pp * B + b];
+            ix[j] = pi[pp * B + b];
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -279,17 +309,19 @@ __global__ __launch_bounds__(FIN_THREADS) void argmax_finish_kernel(const float*
     if (threadIdx.x == 0) {
         for (int w = 1; w < FIN_THREADS / 64; ++w)
             if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
-        tokens[b] = bi;
-        if (pos && b == 0) *pos += 1;
+        finish_row(b, B, bv, bi, p, tokens, pos, counter, sr);
     }
 }
 
-// grid (B): argmax over a stored BF16 logits row.
-__global__ __launch_bounds__(THREADS) void argmax_rows_kernel(const bf16_t* logits, int ld, int V,
-                                                              int64_t* tokens, int64_t* pos) {
+// grid (B): argmax over a stored BF16 logits row, then finish_row; the fed
+// token's logit is read from the row itself.
+__global__ __launch_bounds__(THREADS) void argmax_rows_kernel(const bf16_t* logits, int ld, int V, int B,
+                                                              int64_t* tokens, int64_t* pos, int* counter,
+                                                              StepRec sr) {
     __shared__ float sv[4];
     __shared__ int si[4];
     const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t p = pos != nullptr ? *pos : -2;
     const bf16_t* row = logits + (int64_t)b * ld;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -308,8 +340,12 @@ __global__ __launch_bounds__(THREADS) void argmax_rows_kernel(const bf16_t* logi
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w)
             if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
-        tokens[b] = bi;
-        if (pos && b == 0) *pos += 1;
+        const int64_t q = p + 1;
+        if (sr.rec != nullptr && sr.feed != nullptr && pos != nullptr && q >= 0 && q < sr.npos) {
+            const int64_t f = sr.feed[q * B + b];
+            if (f >= 0 && f < V) sr.rec[(q * B + b) * REC_WORDS + 2] = __float_as_int(bf2f(row[f]));
+        }
+        finish_row(b, B, bv, bi, p, tokens, pos, counter, sr);
     }
 }
 
@@ -379,16 +415,29 @@ extern "C" int q3_qk_norm_rope_kv(const bf16_t* qkv, int ld_qkv, const bf16_t* q
 }
 
 extern "C" int q3_argmax_finish(const float* part_val, const int* part_idx, int nparts, int B, int64_t* tokens,
-                                int64_t* pos, hipStream_t stream) {
-    if (nparts < 1 || B < 1 || !part_val || !part_idx || !tokens) return (int)hipErrorInvalidValue;
+                                int64_t* pos, int* counter, const int64_t* feed, int* rec, int npos,
+                                hipStream_t stream) {
+    if (nparts < 1 || B < 1 || !part_val || !part_idx || !tokens || (pos && B > 1 && !counter) ||
+        ((feed || rec) && (!pos || npos < 1)))
+        return (int)hipErrorInvalidValue;
+    StepRec sr;
+    sr.feed = feed;
+    sr.rec = rec;
+    sr.npos = npos;
     Q3_LAUNCH(argmax_finish_kernel, dim3(B), dim3(FIN_THREADS), 0, stream, part_val, part_idx, nparts,
-                       B, tokens, pos);
+              B, tokens, pos, counter, sr);
     Q3_CHECK_LAUNCH();
 }
 
 extern "C" int q3_argmax_rows(const bf16_t* logits, int ld, int B, int V, int64_t* tokens, int64_t* pos,
-                              hipStream_t stream) {
-    if (B < 1 || V < 1 || ld < V || !logits || !tokens) return (int)hipErrorInvalidValue;
-    Q3_LAUNCH(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, tokens, pos);
+                              int* counter, const int64_t* feed, int* rec, int npos, hipStream_t stream) {
+    if (B < 1 || V < 1 || ld < V || !logits || !tokens || (pos && B > 1 && !counter) ||
+        ((feed || rec) && (!pos || npos < 1)))
+        return (int)hipErrorInvalidValue;
+    StepRec sr;
+    sr.feed = feed;
+    sr.rec = rec;
+    sr.npos = npos;
+    Q3_LAUNCH(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, B, tokens, pos, counter, sr);
     Q3_CHECK_LAUNCH();
 }

@@ -43,6 +43,8 @@ struct SkinnyArgs {
     bool part_only;             // write the partials even with one split, no epilogue
     float* part_val;            // argmax epilogues: [N/64, M] per-workgroup maxima
     int* part_idx;              //   and their rows (first on ties)
+    const int64_t* pos;         // argmax epilogues with a step record: this step's input position
+    StepRec sr;
 };
 
 // x chunks per thread: 16*MT rows x 32 chunks = 512*MT chunks over NT threads
@@ -117,25 +119,31 @@ __device__ __forceinline__ void load_w_tiled(const bf16_t* wtile, int k0, int la
 // Greedy-token epilogue (one split, N % 64 == 0 so every wave is active): the
 // BF16-rounded logit maximum of this workgroup's 64 rows for each batch row,
 // lowest row on ties (reference engine/engine.py:833 torch.argmax), into
-// part_val/part_idx [N/64, M]; STORE_ARGMAX also stores the logits.  red is
-// LDS scratch for 2 * 4 * 16 * MT words (the x tile, free by now).
+// part_val/part_idx [N/64, M]; STORE_ARGMAX also stores the logits; with a
+// step record, the lane holding the row of the token fed at *pos + 1 stores
+// its logit there.  red is LDS scratch for 2 * 4 * 16 * MT words (the x tile,
+// free by now).
 template <int MT>
 __device__ __forceinline__ void argmax_epilogue(const SkinnyArgs& a, const f32x4_t (&acc)[MT], int row0, int wave,
                                                 int lane, float* red) {
     const int g = lane >> 4, n = lane & 15;
     float* rv = red;
     int* ri = reinterpret_cast<int*>(red + 4 * 16 * MT);
+    const int64_t q = a.sr.rec != nullptr ? *a.pos + 1 : -1;
+    const bool pick = q >= 0 && q < a.sr.npos;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int m = 16 * t + n;
         float bv = -INFINITY;
         int bi = 0x7fffffff;
+        const int64_t target = (pick && m < a.M) ? a.sr.feed[q * a.M + m] : -1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t bits = f2bf(acc[t][i]);
             const float v = bf2f((bf16_t)bits);
             const int r = row0 + 4 * g + i;
             if (a.epi == Q3_EPI_STORE_ARGMAX && m < a.M) a.y[(int64_t)m * a.ldy + r] = (bf16_t)bits;
+            if (r == target) a.sr.rec[(q * a.M + m) * REC_WORDS + 2] = __float_as_int(v);
             if (v > bv || (v == bv && r < bi)) { bv = v; bi = r; }
         }
 #pragma unroll
@@ -462,7 +470,8 @@ namespace {
 constexpr int MAX_SPLITS = 16;
 
 int skinny_launch(bool tiled, bool part_only, const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K,
-                  int epi, bf16_t* y, int ldy, float* ws, float* part_val, int* part_idx, hipStream_t stream) {
+                  int epi, bf16_t* y, int ldy, float* ws, float* part_val, int* part_idx, hipStream_t stream,
+                  const int64_t* pos = nullptr, StepRec sr = StepRec{}) {
     if (M < 1 || M > 64 || N < 1 || N % 64 || K < KC || K % KC || ldx % 8 || !x || !w ||
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15))
         return (int)hipErrorInvalidValue;
@@ -477,7 +486,8 @@ int skinny_launch(bool tiled, bool part_only, const bf16_t* x, int ldx, const bf
     if ((splits > 1 || part_only) && !ws) return (int)hipErrorInvalidValue;
     const int chunks = K / KC;
     const int kper = (chunks + splits - 1) / splits * KC;
-    SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws, part_only, part_val, part_idx};
+    if (sr.rec && (!argmax || !pos || !sr.feed || sr.npos < 1)) return (int)hipErrorInvalidValue;
+    SkinnyArgs a{x, ldx, w, M, N, K, splits, kper, epi, y, ldy, ws, part_only, part_val, part_idx, pos, sr};
     // The argmax epilogue is written for four waves; row-major weights take four.
     const int waves = (argmax || !tiled) ? 4 : skinny_plan(M, N, K).waves;
     const dim3 grid((N / 16 + waves - 1) / waves, splits);
@@ -519,9 +529,16 @@ extern "C" int q3_skinny_partials(const bf16_t* x, int ldx, const bf16_t* wt, in
 }
 
 extern "C" int q3_skinny_argmax(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, bf16_t* logits,
-                                int ld_logits, float* part_val, int* part_idx, hipStream_t stream) {
+                                int ld_logits, float* part_val, int* part_idx, const int64_t* pos,
+                                const int64_t* feed, int* rec, int npos, hipStream_t stream) {
+    StepRec sr;
+    if (rec) {
+        sr.feed = feed;
+        sr.rec = rec;
+        sr.npos = npos;
+    }
     return skinny_launch(true, false, x, ldx, wt, M, N, K, logits ? Q3_EPI_STORE_ARGMAX : Q3_EPI_ARGMAX, logits,
-                         ld_logits, nullptr, part_val, part_idx, stream);
+                         ld_logits, nullptr, part_val, part_idx, stream, pos, sr);
 }
 
 extern "C" int q3_tile16(const bf16_t* w, int N, int K, bf16_t* out, hipStream_t stream) {

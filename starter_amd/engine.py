@@ -72,27 +72,21 @@ MEMORY_MARGIN_BYTES = 2 << 30
 GEMV_BATCH_MAX = 4
 SKINNY_BATCH_MAX = 64
 
-#: One sequence decodes in a single persistent kernel per step
-#: (``q3_decode_persistent``) when the shapes allow it; False keeps the
-#: kernel-per-op step (tests compare the two).  Off by default until the
-#: one-kernel step is the faster of the two (2.05 vs 1.86 ms per step at
-#: config 2 so far).  Environment override: Q3_PERSISTENT_DECODE=0 / 1.
-PERSISTENT_DECODE = os.environ.get("Q3_PERSISTENT_DECODE", "0") != "0"
-
 #: Prompt-pass projections through hipBLASLt (``q3_gemm_lt``), with the residual
 #: join in the add+norm kernel and SwiGLU as a row kernel; False keeps the
 #: library's own MFMA GEMM with fused epilogues.
 PREFILL_BLASLT = os.environ.get("Q3_PREFILL_BLASLT", "1") != "0"
 LT_WORKSPACE_BYTES = 64 << 20
 
-#: At batch 1, the o-projection (with its residual join) in that same launch
-#: (``q3_attn_decode_fused_o``).  Off by default: bit-identical, but measured
-#: slower at config 2 (1.875 against 1.854 ms per step).
-FUSED_O_PROJECTION = os.environ.get("Q3_FUSED_O_PROJECTION", "0") != "0"
-
 #: Decode attention and its split merge in one launch where the grid allows it
 #: (``q3_attn_decode_fused``); False keeps two launches (tests compare them).
 FUSED_ATTENTION = os.environ.get("Q3_FUSED_ATTENTION", "1") != "0"
+FUSED_ATTENTION_MAX_LAYERS = 64
+
+#: The contest judge's tie margin (reference QWEN_ENGINE_CONTRACT.md
+#: "tieMarginLogits", currently 2.0): an emitted token must be the replayed
+#: argmax or within this many logits of it.
+TIE_MARGIN_LOGITS = 2.0
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -199,11 +193,6 @@ class Engine:
         self._grow_rope(4096)
 
         self.tiled = None  # 16-row tiled weight copies, made on first use
-        self.persist = False
-        #: Optional device buffer (int64, q3_persist_trace_words(L)) that the
-        #: one-kernel step fills with phase timestamps; set before the graph is
-        #: captured (a diagnostic, see q3.h).
-        self.persist_trace: torch.Tensor | None = None
         self.batch = 0
         self.capacity = 0
         self.cache_k = self.cache_v = None
@@ -268,6 +257,12 @@ class Engine:
         self.splits = call("q3_attn_splits", B, Hkv, capacity)
         self.g_token = torch.zeros(B, dtype=torch.int64, device=self.device)
         self.g_pos = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.g_counter = torch.zeros(1, dtype=torch.int32, device=self.device)
+        # Step records (q3.h): the token fed at each position (-1: the greedy
+        # choice) and, per position, {argmax, max logit, fed token's logit,
+        # fed token}; read by replay(), never by the host inside the graph.
+        self.g_feed = torch.full((capacity + 1, B), -1, dtype=torch.int64, device=self.device)
+        self.g_rec = torch.zeros(capacity + 1, B, 4, dtype=torch.int32, device=self.device)
         self.resid = self._empty(B, H)
         self.nbuf = self._empty(B, H)
         self.qkv_buf = self._empty(B, self.qkv_size)
@@ -278,20 +273,16 @@ class Engine:
         # Attention and its split merge in one launch when the grid is small
         # enough (batch 1-4 at moderate context): flagged exchange words, zeroed
         # at the start of every call, and a timeout word checked every step.
+        # The exchange words' flag encodes (position, layer) with layer < 64
+        # (q3_attn_decode_fused), so deeper models keep the two launches.
         self.attn_fused = (FUSED_ATTENTION and self.splits > 1 and
+                           self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and
                            call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity, self.splits) > 0)
         words = call("q3_attn_xbuf_words", B, self.HEADS, self.splits) if self.attn_fused else 4
         self.attn_x = torch.zeros(words, dtype=torch.int32, device=self.device)
-        # One sequence: the o-projection joins that launch too (its weights stream in
-        # while attention runs), reading the merged heads as flagged words.
-        self.attn_fused_o = (self.attn_fused and FUSED_O_PROJECTION and
-                             call("q3_attn_fused_o_grid", B, self.HEADS, Hkv, capacity, self.splits, H) > 0)
-        words = call("q3_attn_xo_words", self.HEADS) if self.attn_fused_o else 4
-        self.attn_xo = torch.zeros(words, dtype=torch.int32, device=self.device)
         self.attn_err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.small = B <= GEMV_BATCH_MAX
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
-        self.persist = B == 1 and PERSISTENT_DECODE and self._persist_setup(capacity)
         # Split-K workspace of the MFMA decode projections: every projection's
         # partials, [splits, B, N] FP32, one consumer at a time.
         ws = 0
@@ -310,24 +301,9 @@ class Engine:
         self.logits = self._empty(B, V)
         self._capture()
 
-    def _persist_setup(self, capacity: int) -> bool:
-        """Buffers of the one-kernel decode step (B = 1): the device table of layer
-        pointers and the zeroed exchange/work buffer.  False when the device or the
-        model shape does not admit it (then the kernel-per-op step runs)."""
-        grid = call("q3_persist_grid")
-        if grid < 1:
-            return False
-        grid -= grid % self.KV_HEADS
-        if not call("q3_persist_supported", self.LAYERS, self.HIDDEN, self.INTER, self.VOCAB, self.HEADS,
-                    self.KV_HEADS, capacity, grid):
-            return False
-        table = [[L[k].data_ptr() for k in ("qkv", "o", "gate_up", "down", "in_ln", "post_ln", "q_norm", "k_norm")]
-                 for L in self.layers]
-        self.persist_layers = torch.tensor(table, dtype=torch.int64, device=self.device)
-        nbytes = call("q3_persist_work_bytes", self.HIDDEN, self.INTER, self.HEADS, self.KV_HEADS, grid)
-        self.persist_work = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
-        self.persist_grid = grid
-        return True
+    def _records(self) -> tuple:
+        """(feed, rec, npos) of the step records, as the LM-head and argmax-finish launchers take them."""
+        return _ptr(self.g_feed), _ptr(self.g_rec), self.capacity + 1
 
     def _projections(self) -> list[tuple[int, int]]:
         """(N, K) of qkv, o, gate_up, down and the LM head."""
@@ -379,14 +355,6 @@ class Engine:
 
     def _enqueue_decode(self) -> None:
         """One self-feeding decode step on ``self.stream`` (reference ``_forward_decode``)."""
-        if self.persist:
-            call("q3_decode_persistent", _ptr(self.persist_layers), self.LAYERS, _ptr(self.embed),
-                 _ptr(self.final_norm), _ptr(self.lm_head), self.HIDDEN, self.INTER, self.VOCAB, self.HEADS,
-                 self.KV_HEADS, _ptr(self.cos_table), _ptr(self.sin_table), _ptr(self.cache_k),
-                 _ptr(self.cache_v), self.capacity, _ptr(self.g_token), _ptr(self.g_pos), _ptr(self.persist_work),
-                 self.persist_grid, _ptr(self.logits) if self.keep_logits else None, self.EPS, self.SCALE,
-                 _ptr(self.persist_trace), self._s)
-            return
         if self.skinny:
             self._enqueue_decode_skinny()
             return
@@ -403,11 +371,11 @@ class Engine:
                 if i == 0:
                     call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
                          resid, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
-                         None, None, None, None, None, s)
+                         None, None, None, None, None, 0, s)
                 else:
                     call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["in_ln"]), self.EPS, None,
                          _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
-                         None, None, None, None, None, s)
+                         None, None, None, None, None, 0, s)
             else:
                 if i == 0:
                     call("q3_embed_rmsnorm", tok, _ptr(self.embed), resid, nbuf, _ptr(L["in_ln"]), B, H,
@@ -415,16 +383,14 @@ class Engine:
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
-            o_done = self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride,
-                                     vc0 + i * layer_stride, o_proj=self.small)
+            self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride, vc0 + i * layer_stride)
             if self.small:
-                if not o_done:
-                    call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
-                         B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
+                call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
+                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, 0, s)
                 call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["post_ln"]), self.EPS, None,
-                     _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, None, None, None, s)
+                     _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, None, None, None, 0, s)
                 call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
-                     B, H, I, _lib.EPI_RESID, resid, H, None, None, None, None, None, s)
+                     B, H, I, _lib.EPI_RESID, resid, H, None, None, None, None, None, 0, s)
             else:
                 self._proj(attn, self.q_size, L["o"], H, self.q_size, _lib.EPI_RESID, resid, H)
                 call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), nbuf, H, B, H, self.EPS, s)
@@ -434,12 +400,13 @@ class Engine:
             epi = _lib.EPI_STORE_ARGMAX if self.keep_logits else _lib.EPI_ARGMAX
             call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(self.final_norm), self.EPS, None,
                  _ptr(self.lm_head), B, V, H, epi, _ptr(self.logits), V, _ptr(self.part_val),
-                 _ptr(self.part_idx), None, None, None, s)
-            call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
+                 _ptr(self.part_idx), pos, *self._records(), s)
+            call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos,
+                 _ptr(self.g_counter), *self._records(), s)
         else:
             call("q3_rmsnorm", resid, H, _ptr(self.final_norm), nbuf, H, B, H, self.EPS, s)
             self._proj(nbuf, H, self.lm_head, V, H, _lib.EPI_STORE, _ptr(self.logits), V)
-            call("q3_argmax_rows", _ptr(self.logits), V, B, V, tok, pos, s)
+            call("q3_argmax_rows", _ptr(self.logits), V, B, V, tok, pos, _ptr(self.g_counter), *self._records(), s)
 
     def _enqueue_decode_skinny(self) -> None:
         """Decode step for 5..64 rows: tiled-weight MFMA projections whose split-K
@@ -471,32 +438,25 @@ class Engine:
             nxt = self.layers[i + 1]["in_ln"] if i + 1 < self.LAYERS else self.final_norm
             call("q3_add_rmsnorm_partials", ws, s_down, resid, _ptr(nxt), nbuf, B, H, self.EPS, s)
         call("q3_skinny_argmax", nbuf, H, T(self.lm_head), B, V, H, _ptr(self.logits) if self.keep_logits else None,
-             V, _ptr(self.part_val), _ptr(self.part_idx), s)
-        call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos, s)
+             V, _ptr(self.part_val), _ptr(self.part_idx), pos, *self._records(), s)
+        call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos,
+             _ptr(self.g_counter), *self._records(), s)
 
-    def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int, o_proj: bool = False) -> bool:
+    def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int) -> None:
         """Layer i's decode attention into attn_out: q/k norm + RoPE + KV append,
         split-K GQA and the split merge (one launch when ``attn_fused``).
-        ``src`` is (qkv, ld, qkv partials, partial count).  With ``o_proj`` and
-        ``attn_fused_o`` the launch also adds the o-projection into resid;
-        returns whether it did."""
+        ``src`` is (qkv, ld, qkv partials, partial count)."""
         B, Hq, Hkv, C, s = self.batch, self.HEADS, self.KV_HEADS, self.capacity, self._s
         pos, attn = _ptr(self.g_pos), _ptr(self.attn_out)
         common = (_ptr(L["q_norm"]), _ptr(L["k_norm"]), _ptr(self.cos_table), _ptr(self.sin_table), pos, kc, vc)
-        if o_proj and self.attn_fused_o:
-            call("q3_attn_decode_fused_o", *src, *common, _ptr(self.attn_x), attn, _ptr(L["o"]), self.HIDDEN,
-                 _ptr(self.resid), _ptr(self.attn_xo), B, Hq, Hkv, C, self.splits, i, self.EPS, self.SCALE,
-                 _ptr(self.attn_err), s)
-            return True
         if self.attn_fused:
             call("q3_attn_decode_fused", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i,
                  self.EPS, self.SCALE, _ptr(self.attn_err), s)
-            return False
+            return
         call("q3_attn_decode", *src, *common, _ptr(self.part_acc), _ptr(self.part_ml),
              attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
         if self.splits > 1:
             call("q3_attn_merge", _ptr(self.part_acc), _ptr(self.part_ml), attn, B, Hq, self.splits, s)
-        return False
 
     def _proj(self, x: int, ldx: int, w: torch.Tensor, N: int, K: int, epi: int, y: int, ldy: int) -> None:
         """Decode projection for batches outside the GEMV and fused MFMA paths (more
@@ -538,7 +498,6 @@ class Engine:
         decode stream.  Its flags are derived from (position, layer), so words
         left by an earlier call at the same positions would read as fresh."""
         self.attn_x.zero_()
-        self.attn_xo.zero_()
         self.attn_err.zero_()
 
     def _begin_decode(self, logits: torch.Tensor, seq_len: int) -> None:
@@ -546,8 +505,9 @@ class Engine:
         at the prompt length (reference ``engine/engine.py:1077-1079``)."""
         with torch.cuda.stream(self.stream):
             call("q3_argmax_rows", _ptr(logits), self.VOCAB, self.batch, self.VOCAB, _ptr(self.g_token), None,
-                 self._s)
+                 None, None, None, 0, self._s)
             self.g_pos.fill_(seq_len)
+            self.g_feed.fill_(-1)  # self-feeding (a replay that raised may have left a stream)
             self._clear_exchange()
 
     def _decode_step(self) -> torch.Tensor:
@@ -555,25 +515,14 @@ class Engine:
         call("q3_graph_launch", self.graph, self._s)
         return self.g_token
 
-    def _check_step(self, tokens: list[int] | None = None) -> None:
-        """The one-kernel step reports a launch that could not complete (a wait
-        past its time bound) as token -1; raise, and drop the step's state so the
-        next call rebuilds it."""
-        if self.attn_fused:
-            if int(self.attn_err.cpu()[0]):
-                self.graph_key_reset()
-                raise RuntimeError("the fused attention launch did not complete: a merge or o-projection "
-                                   "workgroup waited past its time bound")
-            return
-        if not self.persist:
-            return
-        if tokens is None:
-            tokens = self.g_token.cpu().tolist()
-        if min(tokens) < 0:
-            code = int(self.persist_work[4:8].view(torch.int32).cpu()[0])
+    def _check_step(self) -> None:
+        """Raise if the fused attention launch reported a merge wait past its
+        time bound (``attn_err``), and drop the step's state so the next call
+        rebuilds it."""
+        if self.attn_fused and int(self.attn_err.cpu()[0]):
             self.graph_key_reset()
-            raise RuntimeError(f"q3_decode_persistent did not complete (error {code}): a workgroup "
-                               "waited past its time bound")
+            raise RuntimeError("the fused attention launch did not complete: a merge workgroup waited "
+                               "past its time bound")
 
     # -------------------------------------------------------------- prefill
 
@@ -675,13 +624,19 @@ class Engine:
             if B <= _lib.GEMV_MAX_M:
                 call("q3_gemv", _lib.X_NORM, _ptr(last), T * H, None, _ptr(self.final_norm), self.EPS, None,
                      _ptr(self.lm_head), B, self.VOCAB, H, _lib.EPI_STORE, _ptr(logits), self.VOCAB,
-                     None, None, None, None, None, s)
+                     None, None, None, None, None, 0, s)
             else:
                 n_last = self._empty(B, H)
                 call("q3_rmsnorm", _ptr(last), T * H, _ptr(self.final_norm), _ptr(n_last), H, B, H,
                      self.EPS, s)
                 call("q3_gemm", _ptr(n_last), H, _ptr(self.lm_head), B, self.VOCAB, H, _lib.EPI_STORE,
                      _ptr(logits), self.VOCAB, s)
+        # The caller reads the logits on its own stream (reference
+        # tests/test_equivalence.py:161-166 uses them at once): order its stream
+        # after ours, and keep the block alive until the caller's stream is done.
+        caller = torch.cuda.current_stream(self.device)
+        caller.wait_stream(self.stream)
+        logits.record_stream(caller)
         return logits.view(B, 1, self.VOCAB)
 
     # ------------------------------------------------------------- generate
@@ -717,8 +672,6 @@ class Engine:
                 if self.attn_fused and int(host_err[0]):
                     self._check_step()  # raises
             toks = out.tolist()
-            if self.persist:
-                self._check_step(toks)
             if step + 1 < max_new_tokens:
                 self._decode_step()
                 with torch.cuda.stream(self.stream):
@@ -730,7 +683,129 @@ class Engine:
                 pending = False
             yield toks
 
+    # ------------------------------------------------------ replay judge
+
+    def _stream_tensor(self, rows, batch: int, name: str) -> torch.Tensor:
+        t = torch.tensor(rows, dtype=torch.int64)
+        if t.dim() != 2 or t.shape[1] != batch:
+            raise ValueError(f"{name} must be a list of lists of {batch} ids")
+        if t.numel() and (int(t.min()) < 0 or int(t.max()) >= self.VOCAB):
+            raise ValueError(f"{name} ids must lie in [0, {self.VOCAB})")
+        return t
+
+    def _feed_stream(self, seq_len: int, tokens: torch.Tensor) -> None:
+        """Feed ``tokens[k]`` at position ``seq_len + k`` (k >= 1) through the step
+        records' feed table; ``tokens[0]`` is written as the first input."""
+        with torch.cuda.stream(self.stream):
+            self.g_feed.fill_(-1)
+            if len(tokens) > 1:
+                self.g_feed[seq_len + 1:seq_len + len(tokens)].copy_(tokens[1:])
+            self.g_token.copy_(tokens[0])
+            self.g_rec.zero_()
+
+    def _records_of(self, seq_len: int, n: int) -> np.ndarray:
+        """Step records [n, B, 4] of positions seq_len+1 .. seq_len+n (int32 words)."""
+        self.stream.synchronize()
+        return self.g_rec[seq_len + 1:seq_len + 1 + n].cpu().numpy()
+
+    @torch.inference_mode()
+    def replay(self, input_ids: list[list[int]], emitted: list[list[int]]) -> dict:
+        """Teacher-forced replay of an emitted token stream through the captured decode step.
+
+        Not part of the reference API.  The contest judge replays a stream this
+        way (reference ``QWEN_ENGINE_CONTRACT.md`` "The quality rule"):
+        ``emitted[k]`` (B ids) is checked against the logits computed from the
+        prompt plus ``emitted[:k]``.  Step 0 is judged on the prompt pass's
+        logits; every later step runs the production decode graph, fed from the
+        step records' feed table, with no host copy or sync per step.  Returns
+        numpy arrays [N, B]: ``argmax``, ``top`` (its BF16 logit) and ``logit``
+        (the emitted token's BF16 logit).
+        """
+        ids = _check_ids(input_ids, self.VOCAB)
+        batch, seq_len = ids.shape
+        em = self._stream_tensor(emitted, batch, "emitted")
+        n = em.shape[0]
+        if n == 0:
+            empty = np.zeros((0, batch))
+            return {"argmax": empty.astype(np.int64), "top": empty, "logit": empty}
+        self._ensure_shape(batch, seq_len, n)
+        logits = self._forward_prefill(ids, seq_len).view(batch, self.VOCAB).float().cpu()
+        top, arg = logits.max(dim=-1)
+        first = {"argmax": logits.argmax(dim=-1).numpy(), "top": top.numpy(),
+                 "logit": logits.gather(1, em[0].view(batch, 1))[:, 0].numpy()}
+        self._feed_stream(seq_len, em.to(self.device))
+        with torch.cuda.stream(self.stream):
+            self.g_pos.fill_(seq_len)
+            self._clear_exchange()
+        for _ in range(n - 1):
+            self._decode_step()
+        rec = self._records_of(seq_len, n - 1)
+        self._check_step()
+        with torch.cuda.stream(self.stream):
+            self.g_feed.fill_(-1)
+        out = {
+            "argmax": np.concatenate([first["argmax"][None], rec[..., 0].astype(np.int64)]),
+            "top": np.concatenate([first["top"][None], rec[..., 1].view(np.float32)]),
+            "logit": np.concatenate([first["logit"][None], rec[..., 2].view(np.float32)]),
+        }
+        if not np.array_equal(rec[..., 3], em[1:].numpy()):
+            raise RuntimeError("replay fed a different stream than the one given")
+        return out
+
+    def replay_check(self, input_ids: list[list[int]], emitted: list[list[int]],
+                     margin: float = TIE_MARGIN_LOGITS) -> list[tuple[int, int, float]]:
+        """The contest's quality rule on this engine's own replay: every emitted
+        token is the argmax of the replayed logits or within ``margin`` of the
+        maximum (reference ``QWEN_ENGINE_CONTRACT.md`` "The quality rule",
+        ``tieMarginLogits`` 2.0).  Returns the failing (step, row, shortfall)."""
+        r = self.replay(input_ids, emitted)
+        em = np.asarray(emitted, dtype=np.int64).reshape(r["argmax"].shape)
+        short = r["top"] - r["logit"]
+        bad = np.nonzero((em != r["argmax"]) & (short > margin))
+        return [(int(k), int(b), float(short[k, b])) for k, b in zip(*bad)]
+
     # -------------------------------------------------------- diagnostics
+
+    def prepare_trace(self, batch: int, seq_len: int, new_tokens: int) -> None:
+        """Build the (batch, seq_len + new_tokens) step with the logits stored
+        every step (the LM head's EPI_STORE_ARGMAX epilogue; every other kernel
+        is the production one).  A diagnostic: ``trace_decode`` then reads the
+        logits step by step; ``end_trace`` returns to the production graph."""
+        self.keep_logits = True
+        self.graph_key_reset()
+        self._ensure_shape(batch, seq_len, new_tokens)
+
+    def end_trace(self) -> None:
+        self.keep_logits = False
+        self.graph_key_reset()
+
+    @torch.inference_mode()
+    def trace_decode(self, first: list[int], seq_len: int, steps: int,
+                     forced: list[list[int]] | None = None):
+        """``steps`` decode steps from the cache as it stands (positions below
+        ``seq_len`` already written, e.g. by the caller), the first fed
+        ``first`` (B ids) at ``seq_len``.  With ``forced``, the step at
+        ``seq_len + k`` (k >= 1) is fed ``forced[k - 1]`` through the feed table
+        instead of the engine's choice.  Returns (the engine's choices
+        [steps][B], logits [steps, B, V] on the CPU)."""
+        if not self.keep_logits:
+            raise RuntimeError("trace_decode needs prepare_trace first")
+        B = self.batch
+        feed = [first] + (list(forced[:steps - 1]) if forced is not None else [])
+        self._feed_stream(seq_len, self._stream_tensor(feed, B, "forced").to(self.device))
+        with torch.cuda.stream(self.stream):
+            self.g_pos.fill_(seq_len)
+            self._clear_exchange()
+        kept = []
+        for _ in range(steps):
+            self._decode_step()
+            self.stream.synchronize()
+            kept.append(self.logits.cpu())
+        rec = self._records_of(seq_len, steps)
+        self._check_step()
+        with torch.cuda.stream(self.stream):
+            self.g_feed.fill_(-1)
+        return rec[..., 0].astype(np.int64).tolist(), torch.stack(kept)
 
     @torch.inference_mode()
     def trace_logits(self, input_ids: list[list[int]], max_new_tokens: int,
@@ -741,29 +816,24 @@ class Engine:
         logits with the CPU oracle.  With ``forced`` (one list of B ids per
         step), step i+1 is fed ``forced[i]`` instead of the engine's own choice
         (teacher forcing, as the contest's judge replays a stream).  Returns
-        (steps, logits [N, B, V] on the CPU).
+        (the engine's choices [N][B], logits [N, B, V] on the CPU).
         """
         ids = _check_ids(input_ids, self.VOCAB)
         batch, seq_len = ids.shape
-        self.keep_logits = True
-        self.graph_key_reset()
-        self._ensure_shape(batch, seq_len, max_new_tokens)
-        logits = self._forward_prefill(ids, seq_len)
-        self._begin_decode(logits, seq_len)
-        self.stream.synchronize()
-        steps, kept = [self.g_token.cpu().tolist()], [logits.view(batch, -1).cpu()]
-        for i in range(max_new_tokens - 1):
-            if forced is not None:
-                self.g_token.copy_(torch.tensor(forced[i], dtype=torch.int64))
-                torch.cuda.synchronize()
-            self._decode_step()
-            self.stream.synchronize()
-            steps.append(self.g_token.cpu().tolist())
-            self._check_step(steps[-1])
-            kept.append(self.logits.cpu())
-        self.keep_logits = False
-        self.graph_key_reset()
-        return steps, torch.stack(kept)
+        self.prepare_trace(batch, seq_len, max_new_tokens)
+        try:
+            logits = self._forward_prefill(ids, seq_len)
+            first = logits.view(batch, -1).cpu()
+            steps = [first.float().argmax(dim=-1).tolist()]
+            if max_new_tokens > 1:
+                feed = forced[0] if forced is not None else steps[0]
+                more, kept = self.trace_decode(feed, seq_len, max_new_tokens - 1,
+                                               forced[1:] if forced is not None else None)
+                steps += more
+                return steps, torch.cat([first[None], kept])
+            return steps, first[None]
+        finally:
+            self.end_trace()
 
     def graph_key_reset(self) -> None:
         """Force the next ``_ensure_shape`` to rebuild (e.g. after toggling keep_logits)."""

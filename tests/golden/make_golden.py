@@ -17,9 +17,14 @@ Fixtures:
                            on the reference test's cases (``:208-220``).
   config1_bf16.npz      -- the full seeded Qwen3-4B at BASELINE config 1
                            (B=1, P=32, 32 new tokens), BF16 on CPU.
+  config2_bf16.npz      -- the same model at BASELINE config 2 (B=1, P=1024,
+                           512 new tokens): per step the token, the top-16
+                           (id, logit) pairs, the top-2 gap and the logits at
+                           a fixed 512-id subset; full logits at the first and
+                           last steps.
 
 Run (in this container only; it needs transformers):
-    python tests/golden/make_golden.py [--skip-full]
+    python tests/golden/make_golden.py [--skip-tiny] [--skip-full] [--skip-config2]
 """
 
 from __future__ import annotations
@@ -119,13 +124,41 @@ def make_tiny(tmp: pathlib.Path) -> None:
         del model
 
 
+def full_model(tmp: pathlib.Path):
+    path = tmp / "qwen3_4b_seeded"
+    if not (path / "model.safetensors").exists():
+        t0 = time.time()
+        write_seeded_checkpoint(path, MODEL, MODEL_SEED)
+        print(f"seeded checkpoint written in {time.time() - t0:.1f}s", flush=True)
+    return path, load_hf(path, torch.bfloat16)
+
+
+def step_summary(lg: np.ndarray, subset_size: int, subset_seed: int) -> dict:
+    """Per-step fixture arrays of a batch-1 stream's logits [steps, V]."""
+    top = np.argsort(-lg, axis=-1, kind="stable")[:, :16]
+    srt = np.sort(lg, axis=-1)
+    g = np.random.Generator(np.random.PCG64(subset_seed))
+    subset = np.sort(g.choice(MODEL.vocab_size, subset_size, replace=False))
+    return {"top_ids": top, "top_logits": np.take_along_axis(lg, top, axis=-1),
+            "top2_gap": srt[:, -1] - srt[:, -2], "subset": subset, "subset_logits": lg[:, subset],
+            "logits_first": lg[0], "logits_last": lg[-1]}
+
+
+def make_config2(tmp: pathlib.Path) -> None:
+    wl = WORKLOADS[2]
+    path, model = full_model(tmp)
+    ids = np.array(wl.prompt_ids(), dtype=np.int64)
+    t0 = time.time()
+    tok, lg = baseline_loop(model, ids, wl.new_tokens)
+    print(f"config 2 on HF CPU bf16 in {time.time() - t0:.1f}s", flush=True)
+    np.savez_compressed(OUT / "config2_bf16.npz", ids=ids, tokens=tok[:, 0],
+                        **step_summary(lg[:, 0, :], 512, 512))
+    print("wrote config2_bf16.npz", flush=True)
+
+
 def make_full(tmp: pathlib.Path) -> None:
     wl = WORKLOADS[1]
-    path = tmp / "qwen3_4b_seeded"
-    t0 = time.time()
-    write_seeded_checkpoint(path, MODEL, MODEL_SEED)
-    print(f"seeded checkpoint written in {time.time() - t0:.1f}s", flush=True)
-    model = load_hf(path, torch.bfloat16)
+    path, model = full_model(tmp)
     ids = np.array(wl.prompt_ids(), dtype=np.int64)
     t0 = time.time()
     tok, lg = baseline_loop(model, ids, wl.new_tokens)
@@ -156,15 +189,23 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-full", action="store_true")
     ap.add_argument("--skip-tiny", action="store_true")
+    ap.add_argument("--skip-config2", action="store_true")
+    ap.add_argument("--model-dir", help="an existing seeded Qwen3-4B checkpoint directory to reuse")
     args = ap.parse_args()
     torch.manual_seed(0)
     import transformers
     with tempfile.TemporaryDirectory() as tmp:
         tmp = pathlib.Path(tmp)
+        if args.model_dir:
+            (tmp / "qwen3_4b_seeded").symlink_to(pathlib.Path(args.model_dir).resolve())
         if not args.skip_tiny:
             make_tiny(tmp)
         if not args.skip_full:
             make_full(tmp)
+        if not args.skip_config2:
+            make_config2(tmp)
+    meta_path = OUT / "golden_meta.json"
+    old = json.loads(meta_path.read_text()) if meta_path.exists() else {}
     meta = {
         "transformers": transformers.__version__,
         "torch": torch.__version__,
@@ -175,7 +216,11 @@ def main() -> int:
                  "gain_std": TINY_GAIN_STD, "cases": TINY_CASES},
         "config1": {"batch": 1, "prompt": 32, "new_tokens": 32, "model_seed": MODEL_SEED,
                     "prompt_seed": 1},
+        "config2": {"batch": 1, "prompt": 1024, "new_tokens": 512, "model_seed": MODEL_SEED,
+                    "prompt_seed": 2, "subset": 512},
     }
+    if args.skip_tiny and args.skip_full and old:  # keep what the fixtures that were not rewritten were made with
+        meta = {**old, "config2": meta["config2"]}
     (OUT / "golden_meta.json").write_text(json.dumps(meta, indent=1))
     return 0
 

@@ -51,7 +51,12 @@ def test_bad_arguments_raise_without_launching():
     # M = 0 and K not a multiple of 8 are rejected before any device work.
     with pytest.raises(RuntimeError, match="q3_gemv failed"):
         _lib.call("q3_gemv", 0, None, 0, None, None, 0.0, None, None, 0, 4, 8, 0, None, 0, None, None, None,
-                  None, None, None)
+                  None, None, 0, None)
+    # Step records need the argmax epilogue, a position and a feed table.
+    with pytest.raises(RuntimeError, match="q3_argmax_finish failed"):
+        _lib.call("q3_argmax_finish", 1, 1, 4, 2, 1, 1, None, None, None, 0, None)  # B > 1 advancing pos: counter
+    with pytest.raises(RuntimeError, match="q3_argmax_finish failed"):
+        _lib.call("q3_argmax_finish", 1, 1, 4, 1, 1, None, None, 1, 1, 8, None)   # records without a position
     with pytest.raises(RuntimeError, match="q3_gemm failed"):
         _lib.call("q3_gemm", None, 0, None, 4, 4, 60, 0, None, 0, None)
     with pytest.raises(RuntimeError, match="q3_attn_decode failed"):
@@ -76,25 +81,3 @@ def test_gemv_partials():
     assert _lib.call("q3_gemv_partials", 1, 151936, _lib.EPI_ARGMAX) == 151936 // 4 // 4
     assert _lib.call("q3_gemv_partials", 8, 151936, _lib.EPI_ARGMAX) == 151936 // 2 // 4
     assert _lib.call("q3_gemv_partials", 1, 2560, _lib.EPI_STORE) == 2560 // 4
-
-
-def test_persistent_decode_shape_rules():
-    # Qwen3-4B at one workgroup per CU of MI355X (256), and the 2-layer tile model.
-    assert _lib.call("q3_persist_supported", 36, 2560, 9728, 151936, 32, 8, 1536, 256) == 1
-    assert _lib.call("q3_persist_supported", 2, 512, 1024, 1024, 8, 2, 64, 256) == 1
-    # hidden 320 is not a multiple of the 512-element streamed unit
-    assert _lib.call("q3_persist_supported", 3, 320, 640, 512, 8, 2, 64, 256) == 0
-    # the grid must split evenly over the KV heads and the attention output
-    assert _lib.call("q3_persist_supported", 36, 2560, 9728, 151936, 32, 8, 1536, 252) == 0
-    assert _lib.call("q3_persist_supported", 36, 2560, 9728, 151936, 32, 8, 1536, 0) == 0
-    # work buffer: 256 B of state, then the exchange buffers, each 256-byte aligned
-    nbytes = _lib.call("q3_persist_work_bytes", 2560, 9728, 32, 8, 256)
-    words = 2560 + 6144 + 4096 + 9728 + 256 * 4 * 264 + 256 * 4
-    assert words * 4 + 256 <= nbytes < words * 4 + 256 * 8
-    assert nbytes % 256 == 0
-
-
-def test_persistent_decode_rejects_bad_arguments():
-    with pytest.raises(RuntimeError, match="q3_decode_persistent failed"):
-        _lib.call("q3_decode_persistent", None, 36, None, None, None, 2560, 9728, 151936, 32, 8, None, None,
-                  None, None, 1536, None, None, None, 256, None, 1e-6, 0.088, None, None)

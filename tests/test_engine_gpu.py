@@ -1,27 +1,18 @@
-"""End-to-end parity of ``Engine`` on the GPU against HF's native path.
+"""End-to-end parity of ``Engine`` on the GPU against HF's native path (small models).
 
 Mirrors reference tests/test_equivalence.py (the cases at :208-220, the reset
 test :120-142, shape reuse :174-197 and the prefill logit delta :145-171), but
 in BF16 -- the precision the engine runs in -- against fixtures written from
 transformers' Qwen3ForCausalLM on the CPU (tests/golden/make_golden.py), and
-on the full seeded Qwen3-4B at BASELINE config 1.
+against the CPU oracle for the batch paths.  The full Qwen3-4B workloads are in
+tests/test_workloads_gpu.py.
 
 The bar, per sequence (the contest's quality rule, reference
-QWEN_ENGINE_CONTRACT.md "The quality rule", with a margin of 2*TOL instead of
-2.0 logits):
-  * until the engine's token first differs from HF's, every step's logits are
-    within TOL (max-abs over the vocabulary) of HF's;
-  * at that first differing step, the engine's token has an HF logit within
-    2*TOL of HF's maximum -- i.e. HF's top-2 gap there was below 2*TOL, a
-    near-tie at the precision any reordered BF16 forward has;
-  * teacher-forced on HF's tokens (config 1), every step satisfies both.
-
-TOL is the measured noise floor of a reorder-only GPU forward, not a free
-parameter: on the seeded Qwen3-4B, PyTorch's own GPU path (hipBLASLt GEMMs,
-FP32 attention) differs from HF-on-CPU by max-abs 0.18 / mean 0.029 logits at
-step 0, and the engine by 0.16 / 0.028; on the 3-layer test model the engine
-stays within 0.05.  BF16 logits near 4 are 0.031 apart, so a 1-2 ulp HF gap
-is a tie for any implementation that sums in another order.
+QWEN_ENGINE_CONTRACT.md "The quality rule", with the margin narrowed to
+reordering noise; oracle/compare.py): until the engine's token first differs
+from the reference's, every step's logits are within TOL_TINY (max-abs over the
+vocabulary); at that step the engine's token is within 2 * TOL_TINY of the
+reference's maximum.  On the 3-layer test model the engine stays within 0.05.
 """
 
 import numpy as np
@@ -37,7 +28,6 @@ from starter_amd.checkpoint import load_checkpoint
 pytestmark = pytest.mark.gpu
 
 TOL_TINY = 0.06   # 3 layers, hidden 320
-TOL_FULL = 0.25   # 36 layers, hidden 2560 (measured noise floor 0.16-0.18)
 
 
 def golden(name):
@@ -86,11 +76,12 @@ def test_shape_reuse_at_equal_capacity(tiny_engine):
 
 
 def test_prefill_logit_delta(tiny_engine):
+    """Read at once on the caller's stream, as reference tests/test_equivalence.py:161-166
+    does: _forward_prefill orders the caller's stream after the engine's."""
     g = golden("tiny_bf16")
     ids = torch.from_numpy(g["prefill/ids"])
     tiny_engine._ensure_shape(2, 40, 4)
     mine = tiny_engine._forward_prefill(ids, 40)
-    tiny_engine.stream.synchronize()
     want = g["prefill/logits"]
     delta = np.abs(mine.float().cpu().numpy()[:, 0] - want).max()
     # reference tests/test_equivalence.py:166: delta < 0.05 * max(|logit|, 1)
@@ -110,8 +101,8 @@ def test_prefill_paths_agree(tiny_engine):
         for lt in (True, False, True):
             engine_mod.PREFILL_BLASLT = lt
             tiny_engine._ensure_shape(2, 40, 4)
+            # No sync on the engine's stream: the result is read on the caller's.
             outs.append(tiny_engine._forward_prefill(ids, 40).float().cpu()[:, 0])
-            tiny_engine.stream.synchronize()
     finally:
         engine_mod.PREFILL_BLASLT = saved
     for o in outs:
@@ -160,28 +151,26 @@ def test_fused_mfma_decode_matches_oracle(tile_engine, tile_ckpt, batch):
     assert list(tile_engine.generate(ids, 6)) == steps
 
 
-def _trace_attention(engine, ids, n, fused, fused_o=False):
-    saved = engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION
-    engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION = fused, fused_o
+def _trace_attention(engine, ids, n, fused):
+    saved = engine_mod.FUSED_ATTENTION
+    engine_mod.FUSED_ATTENTION = fused
     try:
         steps, logits = engine.trace_logits(ids, n)
         assert engine.attn_fused == fused
-        assert engine.attn_fused_o == (fused and fused_o and len(ids) == 1)
         tokens = list(engine.generate(ids, n))
         assert int(engine.attn_err.cpu()[0]) == 0
     finally:
-        engine_mod.FUSED_ATTENTION, engine_mod.FUSED_O_PROJECTION = saved
+        engine_mod.FUSED_ATTENTION = saved
     return steps, logits, tokens
 
 
 @pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700), (4, 260), (5, 300)])
 def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, batch, prompt):
     """Contexts long enough for split attention (2..16 splits, grid resident at
-    once) run attention and its split merge as one launch (at batch 1, opt-in,
-    with the o-projection as well).  Same
-    bits as the two-launch path at every step, for trace_logits and generate,
-    across repeated calls (the exchange words are cleared per call), and the
-    oracle's stream.  Batch 5 takes the MFMA (tiled-weight) step."""
+    once) run attention and its split merge as one launch.  Same bits as the
+    two-launch path at every step, for trace_logits and generate, across
+    repeated calls (the exchange words are cleared per call), and the oracle's
+    stream.  Batch 5 takes the MFMA (tiled-weight) step."""
     cfg, tensors = load_checkpoint(tile_ckpt)
     rng = np.random.Generator(np.random.PCG64(900 + batch))
     ids = rng.integers(0, cfg.vocab_size, (batch, prompt)).tolist()
@@ -189,9 +178,6 @@ def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, bat
     s_steps, s_logits, s_tokens = _trace_attention(tile_engine, ids, 8, False)
     assert torch.equal(f_logits, s_logits)
     assert f_steps == s_steps == f_tokens == s_tokens
-    if batch == 1:  # the opt-in o-projection in the same launch: the same bits again
-        o_steps, o_logits, o_tokens = _trace_attention(tile_engine, ids, 8, True, fused_o=True)
-        assert torch.equal(o_logits, s_logits) and o_steps == s_steps == o_tokens
     orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
     want, want_logits = orc.generate(ids, 8, keep_logits=True)
     check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
@@ -211,35 +197,3 @@ def test_deterministic_replays(tiny_engine):
     """Same prompt twice: identical streams (no atomics, fixed reduction orders)."""
     ids = [[5, 6, 7, 8, 9, 10, 11]] * 2
     assert list(tiny_engine.generate(ids, 12)) == list(tiny_engine.generate(ids, 12))
-
-
-def test_config1_full_model_matches_hf(full_ckpt):
-    """Seeded Qwen3-4B, B=1, P=32, 32 greedy tokens."""
-    g = golden("config1_bf16")
-    eng = engine_mod.Engine(str(full_ckpt))
-    ids = g["ids"].tolist()
-    want = g["tokens"].tolist()
-    got = [s[0] for s in eng.generate(ids, 32)]
-
-    def hf_logit(i, tok):
-        hit = np.nonzero(g["top_ids"][i] == tok)[0]
-        return g["top_logits"][i][hit[0]] if len(hit) else -np.inf
-
-    # Free-running: first divergence is a near-tie of HF's.
-    d = next((i for i in range(32) if got[i] != want[i]), 32)
-    if d < 32:
-        short = g["top_logits"][d][0] - hf_logit(d, got[d])
-        assert short <= 2 * TOL_FULL, (d, got[d], want[d], short)
-    # Teacher-forced on HF's tokens: every step within TOL and a near-argmax choice.
-    steps, logits = eng.trace_logits(ids, 32, forced=[[t] for t in want])
-    lg = logits[:, 0].float().numpy()
-    first = np.abs(lg[0] - g["logits_first"]).max()
-    last = np.abs(lg[-1] - g["logits_last"]).max()
-    sub = np.abs(lg[:, g["subset"]] - g["subset_logits"]).max(axis=1)
-    shorts = [g["top_logits"][i][0] - hf_logit(i, steps[i][0]) for i in range(32)]
-    print(f"config1: free-running tokens equal through step {d - 1}; teacher-forced logit "
-          f"max-abs first {first:.3f} last {last:.3f} subset {sub.max():.3f}; "
-          f"argmax matches HF at {sum(s[0] == w for s, w in zip(steps, want))}/32 steps, "
-          f"worst shortfall {max(shorts):.4f}", flush=True)
-    assert first <= TOL_FULL and last <= TOL_FULL and sub.max() <= TOL_FULL
-    assert max(shorts) <= 2 * TOL_FULL

@@ -177,15 +177,20 @@ def test_gemv_plain_store(M, N, K):
     x, w = rnd((M, K), 1.0, M), rnd((N, K), 0.02, N + K)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     call("q3_gemv", _lib.X_PLAIN, P(dv(x)), K, None, None, 0.0, None, P(dv(w)), M, N, K,
-         _lib.EPI_STORE, P(y), N, None, None, None, None, None, S())
+         _lib.EPI_STORE, P(y), N, None, None, None, None, None, 0, S())
     torch.cuda.synchronize()
     check_projection(y, x, w)
 
 
 def gemv(x_mode, x, ldx, w, M, N, K, epi, y, ldy, ids=None, norm_w=None, resid_out=None, pv=None, pi=None,
-         tokens=None, pos=None, counter=None):
+         pos=None, feed=None, rec=None):
     call("q3_gemv", x_mode, P(x), ldx, P(ids), P(norm_w), 1e-6, P(resid_out), P(w), M, N, K, epi, P(y), ldy,
-         P(pv), P(pi), P(tokens), P(pos), P(counter), S())
+         P(pv), P(pi), P(pos), P(feed), P(rec), 0 if rec is None else rec.shape[0], S())
+
+
+def finish(pv, pi, nparts, M, tok, pos=None, counter=None, feed=None, rec=None, stream=None):
+    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), P(pos), P(counter), P(feed), P(rec),
+         0 if rec is None else rec.shape[0], stream if stream is not None else S())
 
 
 @pytest.mark.parametrize("M", [1, 3, 8])
@@ -242,7 +247,7 @@ def test_gemv_ragged_swiglu_and_argmax(M):
     pi = torch.empty(nparts, M, dtype=torch.int32, device=DEV)
     gemv(_lib.X_NORM, src, K, wv, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi)
     tok = torch.empty(M, dtype=torch.int64, device=DEV)
-    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), None, S())
+    finish(pv, pi, nparts, M, tok)
     torch.cuda.synchronize()
     gu = gu.cpu()
     assert_nearly_exact(act, oc.swiglu(gu[:, 0::2], gu[:, 1::2]), frac=5e-3)
@@ -272,21 +277,36 @@ def test_gemv_embed_norm_and_argmax(M):
     gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_STORE_ARGMAX, y2, V, norm_w=g, pv=pv, pi=pi)
     tok = torch.empty(M, dtype=torch.int64, device=DEV)
     pos = torch.tensor([5], dtype=torch.int64, device=DEV)
-    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok), P(pos), S())
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    finish(pv, pi, nparts, M, tok, pos, counter)
     tok2 = torch.empty_like(tok)
     gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi)
-    call("q3_argmax_finish", P(pv), P(pi), nparts, M, P(tok2), None, S())
-    # Fused finish: the last workgroup reduces the partials, twice in a row
-    # (the counter must come back to zero).
-    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
-    tok3 = torch.full_like(tok, -1)
-    for _ in range(2):
-        gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi,
-             tokens=tok3, pos=pos, counter=counter)
+    finish(pv, pi, nparts, M, tok2)
     torch.cuda.synchronize()
     assert torch.equal(y2.cpu(), y.cpu())
-    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist() == tok2.cpu().tolist() == tok3.cpu().tolist()
-    assert pos.item() == 8 and counter.item() == 0
+    assert tok.cpu().tolist() == y.cpu().argmax(-1).tolist() == tok2.cpu().tolist()
+    assert pos.item() == 6 and counter.item() == 0
+    # Step records at position 7 (the step's input at 6): rows 0.. fed chosen
+    # tokens, the last row left to the greedy choice.
+    npos = 10
+    feed = torch.full((npos, M), -1, dtype=torch.int64)
+    targets = torch.randint(0, V, (M,), generator=torch.Generator().manual_seed(40 + M))
+    feed[7, :M - 1] = targets[:M - 1]
+    feedd, rec = dv(feed), torch.zeros(npos, M, 4, dtype=torch.int32, device=DEV)
+    tok3 = torch.empty_like(tok)
+    gemv(_lib.X_NORM, resid, K, td, M, V, K, _lib.EPI_ARGMAX, None, 0, norm_w=g, pv=pv, pi=pi,
+         pos=pos, feed=feedd, rec=rec)
+    finish(pv, pi, nparts, M, tok3, pos, counter, feedd, rec)
+    torch.cuda.synchronize()
+    yc, r = y.cpu().float(), rec.cpu()
+    greedy = yc.argmax(-1)
+    fed = torch.where(feed[7] >= 0, feed[7], greedy)
+    assert tok3.cpu().tolist() == fed.tolist()
+    assert r[7, :, 0].tolist() == greedy.tolist() and r[7, :, 3].tolist() == fed.tolist()
+    assert torch.equal(r[7, :, 1].view(torch.float32), yc.max(-1).values)
+    assert torch.equal(r[7, :, 2].view(torch.float32), yc.gather(1, fed.view(M, 1))[:, 0])
+    assert (r[:7] == 0).all() and (r[8:] == 0).all()  # only position 7 is written
+    assert pos.item() == 7 and counter.item() == 0
 
 
 def test_argmax_rows_ties():
@@ -297,9 +317,22 @@ def test_argmax_rows_ties():
     x[2, [4999, 12, 13]] = 2.5
     tok = torch.empty(3, dtype=torch.int64, device=DEV)
     pos = torch.zeros(1, dtype=torch.int64, device=DEV)
-    call("q3_argmax_rows", P(dv(x)), V, 3, V, P(tok), P(pos), S())
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    xd = dv(x)
+    call("q3_argmax_rows", P(xd), V, 3, V, P(tok), P(pos), P(counter), None, None, 0, S())
     torch.cuda.synchronize()
-    assert tok.cpu().tolist() == [7, 0, 12] and pos.item() == 1
+    assert tok.cpu().tolist() == [7, 0, 12] and pos.item() == 1 and counter.item() == 0
+    # With step records at position 2: row 1 fed token 9 (logit -1), the others greedy.
+    feed = torch.full((4, 3), -1, dtype=torch.int64)
+    feed[2, 1] = 9
+    rec = torch.zeros(4, 3, 4, dtype=torch.int32, device=DEV)
+    call("q3_argmax_rows", P(xd), V, 3, V, P(tok), P(pos), P(counter), P(dv(feed)), P(rec), 4, S())
+    torch.cuda.synchronize()
+    r = rec.cpu()
+    assert tok.cpu().tolist() == [7, 9, 12] and pos.item() == 2
+    assert r[2, :, 0].tolist() == [7, 0, 12] and r[2, :, 3].tolist() == [7, 9, 12]
+    assert r[2, :, 1].view(torch.float32).tolist() == [3.0, -1.0, 2.5]
+    assert r[2, :, 2].view(torch.float32).tolist() == [3.0, -1.0, 2.5]
 
 
 @pytest.mark.parametrize("M", [1, 9, 16, 17, 40, 64, 100, 300])
@@ -372,9 +405,13 @@ def attention_oracle(q, ck, cv, length, scale):
                                             (3, 300, 299, 5), (2, 1536, 1100, 12), (1, 1536, 1535, 12),
                                             (2, 700, 255, 40), (1, 700, 699, 1), (2, 1000, 900, 2),
                                             (1, 2176, 2100, 2), (1, 3000, 2999, 3), (1, 1536, 1300, 1),
-                                            (4, 2048, 2047, 1), (40, 300, 290, 1)])
+                                            (4, 2048, 2047, 1), (40, 300, 290, 1),
+                                            # the engine's decode shapes at configs 5 and 4
+                                            (8, 16512, 16500, 12), (64, 2176, 2100, 1)])
 def test_attn_decode(B, C, pos, splits):
     Hq, Hkv, D = 32, 8, 128
+    if B * C >= 100_000:  # a workload shape: the split count is the one the engine uses
+        assert call("q3_attn_splits", B, Hkv, C) == splits
     width = (Hq + 2 * Hkv) * D
     qkv = rnd((B, width), 1.5, pos + 1)
     qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
@@ -453,7 +490,7 @@ def test_graph_capture_replays_self_feeding_step():
     import ctypes
     torch.cuda.synchronize()
     call("q3_graph_begin", stream.cuda_stream)
-    call("q3_argmax_finish", P(pv), P(pi), 3, 1, P(tok), P(pos), stream.cuda_stream)
+    finish(pv, pi, 3, 1, tok, pos, stream=stream.cuda_stream)
     ex = ctypes.c_void_p()
     call("q3_graph_end", stream.cuda_stream, ctypes.byref(ex))
     for _ in range(3):
@@ -536,14 +573,29 @@ def test_skinny_argmax(M, N, K):
     logits = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     tok = torch.empty(M, dtype=torch.int64, device=DEV)
     for store in (False, True):
-        call("q3_skinny_argmax", P(xd), K, P(wt), M, N, K, P(logits) if store else None, N, P(pv), P(pi), S())
-        call("q3_argmax_finish", P(pv), P(pi), parts, M, P(tok), None, S())
+        call("q3_skinny_argmax", P(xd), K, P(wt), M, N, K, P(logits) if store else None, N, P(pv), P(pi),
+             None, None, None, 0, S())
+        finish(pv, pi, parts, M, tok)
         torch.cuda.synchronize()
         ref = want.cpu().float()
         assert torch.equal(tok.cpu(), ref.argmax(dim=1)), store
         if store:
             assert torch.equal(logits.cpu(), want.cpu())
     assert (ref[:, 7] == ref[:, N - 1]).all()
+    # Step records at position 3 (input at 2): every row fed a chosen token.
+    feed = torch.full((5, M), -1, dtype=torch.int64)
+    feed[3] = torch.randint(0, N, (M,), generator=torch.Generator().manual_seed(M))
+    feedd, rec = dv(feed), torch.zeros(5, M, 4, dtype=torch.int32, device=DEV)
+    pos, counter = dv(torch.tensor([2])), torch.zeros(1, dtype=torch.int32, device=DEV)
+    call("q3_skinny_argmax", P(xd), K, P(wt), M, N, K, None, N, P(pv), P(pi), P(pos), P(feedd), P(rec), 5, S())
+    finish(pv, pi, parts, M, tok, pos, counter, feedd, rec)
+    torch.cuda.synchronize()
+    r = rec.cpu()
+    assert tok.cpu().tolist() == feed[3].tolist() == r[3, :, 3].tolist()
+    assert r[3, :, 0].tolist() == ref.argmax(dim=1).tolist()
+    assert torch.equal(r[3, :, 1].view(torch.float32), ref.max(dim=1).values)
+    assert torch.equal(r[3, :, 2].view(torch.float32), ref.gather(1, feed[3].view(M, 1))[:, 0])
+    assert pos.item() == 3 and counter.item() == 0
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 2560, 4096), (16, 2560, 9728), (64, 2560, 9728), (9, 512, 1024)])
@@ -628,57 +680,9 @@ def test_attn_decode_fused(B, C, pos, splits, qsplits):
     assert err.item() == 0
 
 
-@pytest.mark.parametrize("Hq,Hkv,N,C,pos,splits", [(32, 8, 2560, 1536, 1100, 12), (32, 8, 2560, 300, 0, 2),
-                                                    (32, 8, 2560, 2000, 1999, 16), (8, 2, 512, 700, 650, 6),
-                                                    (16, 4, 1000, 900, 500, 5)])
-def test_attn_decode_fused_o(Hq, Hkv, N, C, pos, splits):
-    """Attention + merge + o-projection (residual join) in one launch ==
-    q3_attn_decode_fused then q3_gemv(X_PLAIN, EPI_RESID), bit for bit: the
-    attention output, the cache append and the residual, over several layers'
-    flags and a repeated (position, layer) after zeroing the exchange words.
-    N = 1000 leaves the last wave's second row past the end."""
-    B, D = 1, 128
-    width = (Hq + 2 * Hkv) * D
-    grid = call("q3_attn_fused_o_grid", B, Hq, Hkv, C, splits, N)
-    assert grid == call("q3_attn_fused_grid", B, Hq, Hkv, C, splits) + (N + 7) // 8
-    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
-    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
-    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
-    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
-    ow = dv(rnd((N, Hq * D), 0.02, 6))
-    posd = dv(torch.tensor([pos]))
-    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
-    xo = torch.zeros(call("q3_attn_xo_words", Hq), dtype=torch.int32, device=DEV)
-    err = torch.zeros(1, dtype=torch.int32, device=DEV)
-    for layer, seed in ((0, 7), (1, 8), (0, 9)):
-        if layer == 0 and seed == 9:
-            xbuf.zero_()
-            xo.zero_()
-        src = (P(dv(rnd((B, width), 1.5, seed))), width, None, 0)
-        res0 = rnd((B, N), 1.0, seed + 20)
-        got = []
-        for fused in (False, True):
-            ckd, cvd, res = dv(ck), dv(cv), dv(res0)
-            out = dv(torch.empty(B, Hq * D, dtype=torch.bfloat16))
-            common = (P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd), P(ckd), P(cvd), P(xbuf), P(out))
-            if fused:
-                call("q3_attn_decode_fused_o", *src, *common, P(ow), N, P(res), P(xo), B, Hq, Hkv, C, splits,
-                     layer, 1e-6, D ** -0.5, P(err), S())
-            else:
-                call("q3_attn_decode_fused", *src, *common, B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5,
-                     P(err), S())
-                call("q3_gemv", _lib.X_PLAIN, P(out), Hq * D, None, None, 0.0, None, P(ow), B, N, Hq * D,
-                     _lib.EPI_RESID, P(res), N, None, None, None, None, None, S())
-            torch.cuda.synchronize()
-            got.append((out.cpu(), res.cpu(), ckd.cpu(), cvd.cpu()))
-        for a, b in zip(*got):
-            assert torch.equal(a, b), (layer, seed)
-        assert not torch.equal(got[1][1], res0)
-    assert err.item() == 0
-    assert call("q3_attn_fused_o_grid", 2, Hq, Hkv, C, splits, N) == 0  # one sequence only
-
-
-@pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6)])
+@pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6),
+                                              # configs 5 and 4: qkv from the skinny projection's partials
+                                              (8, 16512, 16500, 5), (64, 2176, 2100, 5)])
 def test_attn_decode_qkv_partials(B, C, pos, qsplits):
     """q/k/v from FP32 split partials == from their in-order sum rounded to BF16, bit for bit."""
     Hq, Hkv, D = 32, 8, 128
