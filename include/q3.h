@@ -107,6 +107,22 @@ int q3_skinny(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K
  * instruction reads 1 KB of contiguous weights. */
 int q3_skinny_tiled(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
                     int epi, uint16_t *y, int ldy, float *ws, hipStream_t stream);
+/* q3_skinny_tiled with no workspace argument and no allocation: the split-K
+ * partials live in a file-scope device array of q3_skinny_scratch_floats()
+ * floats (8 MiB) that each GPU holds for the life of the process.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under hipGraph capture, serving loops and harnesses that forbid hipMalloc).
+ * Same arguments and result, bit for bit, as q3_skinny_tiled; shapes whose
+ * q3_skinny_ws_floats(M, N, K) exceeds the array return hipErrorOutOfMemory
+ * before any launch.  Every call on one GPU shares that GPU's array (it keeps
+ * the last call's partials; each call writes every partial it reads, so
+ * nothing needs clearing): calls that overlap on one GPU -- concurrent
+ * streams or threads -- race and must be serialised by the caller.  The
+ * array's device address is looked up on a device's first call (make that
+ * first call outside stream capture). */
+int q3_skinny_tiled_noalloc(const uint16_t *x, int ldx, const uint16_t *wt, int M, int N, int K,
+                            int epi, uint16_t *y, int ldy, hipStream_t stream);
+int q3_skinny_scratch_floats(void);
 /* q3_skinny_tiled without an epilogue: the FP32 split partials
  * ws [q3_skinny_splits(M, N, K), M, N] (one split included), for consumers
  * that sum them in split order: q3_add_rmsnorm_partials, q3_attn_decode. */

@@ -36,6 +36,8 @@ SIGNATURES = {
     "q3_skinny": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_tiled": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_partials": [_P, _I, _P, _I, _I, _I, _P, _P],
+    "q3_skinny_tiled_noalloc": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P],
+    "q3_skinny_scratch_floats": [],
     "q3_skinny_argmax": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _I, _P],
     "q3_tile16": [_P, _I, _I, _P, _P],
     "q3_skinny_splits": [_I, _I, _I],
@@ -64,7 +66,7 @@ _RESTYPES = {"q3_error_string": ctypes.c_char_p}
 
 #: entry points that return a count, not an error code
 _COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words",
-           "q3_skinny_splits", "q3_skinny_ws_floats"}
+           "q3_skinny_splits", "q3_skinny_ws_floats", "q3_skinny_scratch_floats"}
 
 _LIB: ctypes.CDLL | None = None
 

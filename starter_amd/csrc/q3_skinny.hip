@@ -22,6 +22,8 @@
 #include "q3_common.hpp"
 #include "q3.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int THREADS = 256;
@@ -520,6 +522,54 @@ extern "C" int q3_skinny(const bf16_t* x, int ldx, const bf16_t* w, int M, int N
 extern "C" int q3_skinny_tiled(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, int epi, bf16_t* y,
                                int ldy, float* ws, hipStream_t stream) {
     if (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) return (int)hipErrorInvalidValue;
+    return skinny_launch(true, false, x, ldx, wt, M, N, K, epi, y, ldy, ws, nullptr, nullptr, stream);
+}
+
+// ---- the no-allocation variant of q3_skinny_tiled --------------------------
+//
+// Split-K partials in a file-scope device array instead of a caller workspace,
+// for callers that cannot allocate.  Each device holds its own copy for the
+// life of the process; the host never passes the array's name to a kernel
+// (that is a host-side stand-in, not a device address): it looks up the
+// address once per device with that device current, and passes that.
+constexpr int SCRATCH_FLOATS = 2 * 1024 * 1024;  // 8 MiB: qkv at 64 rows needs 1,966,080
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex scratch_mu;
+float* scratch_dev[SCRATCH_DEVICES];  // scratch's address on each device, once looked up
+
+hipError_t scratch_on_current_device(float** out) {
+    int dev = 0;
+    hipError_t rc = hipGetDevice(&dev);
+    if (rc != hipSuccess) return rc;
+    if (dev < 0 || dev >= SCRATCH_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (rc != hipSuccess) return rc;
+        scratch_dev[dev] = static_cast<float*>(p);
+    }
+    *out = scratch_dev[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int q3_skinny_scratch_floats(void) { return SCRATCH_FLOATS; }
+
+extern "C" int q3_skinny_tiled_noalloc(const bf16_t* x, int ldx, const bf16_t* wt, int M, int N, int K, int epi,
+                                       bf16_t* y, int ldy, hipStream_t stream) {
+    if (epi == Q3_EPI_ARGMAX || epi == Q3_EPI_STORE_ARGMAX) return (int)hipErrorInvalidValue;
+    if (M < 1 || M > 64 || N < 64 || N % 64 || K < KC || K % KC) return (int)hipErrorInvalidValue;
+    // Every partial the reduce reads is written first by this call: nothing to clear.
+    if (q3_skinny_ws_floats(M, N, K) > SCRATCH_FLOATS) return (int)hipErrorOutOfMemory;
+    float* ws = nullptr;
+    const hipError_t rc = scratch_on_current_device(&ws);
+    if (rc != hipSuccess) return (int)rc;
     return skinny_launch(true, false, x, ldx, wt, M, N, K, epi, y, ldy, ws, nullptr, nullptr, stream);
 }
 

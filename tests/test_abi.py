@@ -81,3 +81,15 @@ def test_gemv_partials():
     assert _lib.call("q3_gemv_partials", 1, 151936, _lib.EPI_ARGMAX) == 151936 // 4 // 4
     assert _lib.call("q3_gemv_partials", 8, 151936, _lib.EPI_ARGMAX) == 151936 // 2 // 4
     assert _lib.call("q3_gemv_partials", 1, 2560, _lib.EPI_STORE) == 2560 // 4
+
+
+def test_noalloc_projection_rejects_oversize_before_any_launch():
+    """q3_skinny_tiled_noalloc checks its fixed 8 MiB array against the shape's
+    split partials before touching a device (hipErrorOutOfMemory)."""
+    M, N, K = 64, 4160, 10240
+    assert _lib.call("q3_skinny_scratch_floats") == 2 * 1024 * 1024
+    assert _lib.call("q3_skinny_ws_floats", M, N, K) > _lib.call("q3_skinny_scratch_floats")
+    rc = _lib.lib().q3_skinny_tiled_noalloc(1, K, 1, M, N, K, _lib.EPI_STORE, 1, N, None)
+    assert rc == 2  # hipErrorOutOfMemory
+    # The largest decode projection (qkv at 64 rows) fits.
+    assert _lib.call("q3_skinny_ws_floats", 64, 6144, 2560) <= _lib.call("q3_skinny_scratch_floats")
