@@ -56,6 +56,11 @@ from .checkpoint import Qwen3Config, load_checkpoint
 
 DEVICE = "cuda:0"
 
+#: The weights' dtype (reference ``engine/engine.py`` ``LOAD_DTYPE``, which its
+#: CPU test sets to float32).  The kernels compute in BF16 only, so any other
+#: value is refused at construction rather than silently ignored.
+LOAD_DTYPE = torch.bfloat16
+
 #: Prompt tokens (batch x prompt) per prefill chunk.  The reference caps a
 #: chunk at 16384 tokens for an 80 GB H100 (``engine/engine.py:34``); with
 #: 288 GB the full 131072-token prompts of the benchmark fit in one pass
@@ -135,8 +140,11 @@ class Engine:
     """Greedy Qwen3 decode engine; dimensions come from the checkpoint's config."""
 
     def __init__(self, model_path: str) -> None:
-        if not torch.cuda.is_available():
-            raise RuntimeError("Engine needs a ROCm GPU (gfx950); none is visible")
+        if LOAD_DTYPE != torch.bfloat16:
+            raise ValueError(f"LOAD_DTYPE {LOAD_DTYPE}: the gfx950 kernels compute in BF16 only")
+        if not torch.cuda.is_available() or not str(DEVICE).startswith("cuda"):
+            raise RuntimeError(f"Engine needs a ROCm GPU (gfx950) as DEVICE, got {DEVICE!r} "
+                               f"(visible: {torch.cuda.is_available()}); there is no CPU path")
         _lib.lib()  # fail now, not mid-generation, if the kernels are not built
         self.device = torch.device(DEVICE)
         torch.cuda.set_device(self.device)

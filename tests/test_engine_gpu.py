@@ -197,3 +197,32 @@ def test_deterministic_replays(tiny_engine):
     """Same prompt twice: identical streams (no atomics, fixed reduction orders)."""
     ids = [[5, 6, 7, 8, 9, 10, 11]] * 2
     assert list(tiny_engine.generate(ids, 12)) == list(tiny_engine.generate(ids, 12))
+
+
+def test_reference_harness_path(tiny_ckpt):
+    """Through the archive-root engine/engine.py as reference tests/test_equivalence.py:22-27,
+    90-92,97-103 drives it: the engine directory on sys.path, `import engine`, the chunk size
+    patched on that module, then Engine(path) and generate, against HF's stream."""
+    import importlib
+    import pathlib
+    import sys
+
+    root = pathlib.Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root / "engine"))
+    try:
+        sys.modules.pop("engine", None)
+        mod = importlib.import_module("engine")
+    finally:
+        sys.path.remove(str(root / "engine"))
+    name, b, p, n, chunk = next(c for c in TINY_CASES if c[0] == "chunked_tail")
+    g = golden("tiny_bf16")
+    original = mod.PREFILL_CHUNK_TOKENS
+    mod.PREFILL_CHUNK_TOKENS = chunk
+    try:
+        eng = mod.Engine(str(tiny_ckpt))
+        got = list(eng.generate(g[f"{name}/ids"].tolist(), n))
+        steps, logits = eng.trace_logits(g[f"{name}/ids"].tolist(), n)
+    finally:
+        mod.PREFILL_CHUNK_TOKENS = original
+    assert got == steps
+    check_stream(got, logits.float().numpy(), g[f"{name}/tokens"], g[f"{name}/logits"], TOL_TINY)
