@@ -74,21 +74,16 @@ int q3_gemv(int x_mode, const uint16_t *x, int ldx, const int64_t *ids,
             const int64_t *pos, const int64_t *feed, int32_t *rec, int npos, hipStream_t stream);
 int q3_gemv_partials(int M, int N, int epi);
 
-/* Dense projection for any M (MFMA, LDS-tiled): y = epi(x . W^T), epi in
- * {STORE, RESID, SWIGLU}.  Replaces F.linear / cuBLAS in prefill and at decode
- * batches above 8 (engine.py:439,450,803).  K % 64 == 0; x, W 16-byte aligned. */
+/* Dense projection for any M on MFMA: y = epi(x . W^T), epi in {STORE, RESID,
+ * SWIGLU}.  Replaces F.linear / cuBLAS in the prompt pass and at decode batches
+ * above 64 (engine.py:439,450,803).  With q3_gemm_tiles_wide(M, N) the
+ * 256 x 256-tile kernel (eight waves, direct global-to-LDS loads) runs, else
+ * 16..128-row tiles.  K % 64 == 0; N % 4 == 0; ldx >= K, ldx % 8 == 0;
+ * ldy % 4 == 0 (SWIGLU writes N/2 columns); x, W 16-byte and y 8-byte
+ * aligned. */
 int q3_gemm(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, hipStream_t stream);
-
-/* Prompt-pass projection through hipBLASLt: y = bf16(x . W^T), FP32
- * accumulation, one rounding (F.linear -> cuBLAS, engine.py:450,803).
- * workspace: device memory of workspace_bytes for the library (may be 0
- * bytes).  Creates the library handle on a device's first call (allocates:
- * not under stream capture).  hipErrorNotSupported when the library offers no
- * algorithm for the shape within the workspace. */
-int q3_gemm_lt(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
-               uint16_t *y, int ldy, void *workspace, size_t workspace_bytes,
-               hipStream_t stream);
+int q3_gemm_tiles_wide(int M, int N);
 
 /* act[r, j] = bf16(bf16(silu(g)) * u), (g, u) = gu[r, 2j], gu[r, 2j + 1]:
  * swiglu (fused.py:872; engine.py:464) on interleaved gate/up rows [rows, 2I].

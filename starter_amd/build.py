@@ -74,7 +74,7 @@ def build_hip_lib() -> pathlib.Path:
     with ThreadPoolExecutor(jobs) as pool:
         list(pool.map(lambda so: _run([hipcc, *compile_flags, "-c", str(so[0]), "-o", str(so[1])]),
                       zip(HIP_SOURCES, objs)))
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp), "-lhipblaslt"])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, target)
     return target
 

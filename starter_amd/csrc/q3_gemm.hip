@@ -1,21 +1,231 @@
-// Dense BF16 projection y = epi(x . W^T) on gfx950 MFMA (v_mfma_f32_16x16x32_bf16),
-// for the prompt pass and for decode batches above 8 rows.
+// Dense BF16 projection y = epi(x . W^T) on gfx950 MFMA (v_mfma_f32_16x16x32_bf16):
+// the prompt pass, and decode batches above 64 rows.
 //
 // Reference: engine/engine.py:431-450,803 (F.linear -> cuBLAS for prefill and
 // for more than 32 rows).  FP32 accumulation, one rounding to BF16, then the
 // same epilogues as the decode GEMV (residual join, SwiGLU on interleaved
-// gate/up rows).
+// gate/up rows), so the prompt pass needs no separate row kernels.
 //
-// Tiling: a workgroup (4 waves) owns a BM x BN output tile and walks K in
-// steps of 64.  x and W tiles are staged through LDS (128-byte rows, 16-byte
-// chunks XOR-swizzled so the 16 rows an MFMA operand read touches fall in
-// distinct bank groups); the next K step's global loads are issued before the
-// current step's MFMAs.  Operands: A = x rows (m = token), B = W rows
-// (n = output column), so a lane's C values are 4 tokens of one column.
+// Two tilings, picked by the number of output tiles:
+//
+// * wide (the prompt pass): a 512-thread workgroup owns a 256 x 256 output
+//   tile; eight waves, two per SIMD, each a 128 (token) x 64 (weight row)
+//   sub-tile whose 32 FP32 accumulator blocks stay in registers.  K advances
+//   64 at a time through two 64 KB LDS stages filled by global_load_lds_dwordx4
+//   (global memory straight into LDS, no register round trip).  Within a step
+//   the MFMAs of one 32-wide k half run while the fragments of the next half
+//   load (one LDS read per two MFMAs); a single barrier per step separates
+//   "stage kt+1 has landed" from "stage kt may be refilled".  Each 128-byte
+//   tile row is one contiguous 128-byte global read (eight lanes), and its
+//   16-byte chunks are XOR-swizzled so the operand reads (16 rows, one chunk)
+//   are free of LDS bank conflicts.  Workgroup w runs on XCD w % 8; each XCD
+//   takes a contiguous range of tiles, walked in groups of four token tiles
+//   across the weight tiles, so the XCD's L2 serves the operands its
+//   concurrent workgroups share.
+//
+// * narrow (few tiles: small prompts and decode batches above 64): 256
+//   threads, BM x BN tiles of up to 128 x 128, LDS staged through registers.
+//
+// Operands: A = W rows (n), B = x rows (m), so a lane's four C values are four
+// consecutive output columns of one token row (8-byte stores; both halves of a
+// SwiGLU pair in one lane).
 #include "q3_common.hpp"
 #include "q3.h"
 
 namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; expcnt
+// and lgkmcnt left at their maxima, so they are not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 16 bytes per lane from sbase + voff straight into LDS at m0 + 16 * lane
+// (global_load_lds_dwordx4, scalar base + 32-bit lane offset).  Written as asm
+// because the compiler otherwise makes every later LDS read wait for all
+// direct-to-LDS loads in flight, which serialises the pipeline; the kernel
+// waits for exactly the stage it needs (vmcnt) and then takes a barrier.
+// Nothing else in these kernels uses m0 (clang warns that a clobbered m0 is
+// not restored for code that would).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load_to_lds(const void* sbase, uint32_t voff, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0\n"
+                 :
+                 : "s"(sbase), "v"(voff), "s"(m0)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((lds_ptr_t)p);
+}
+
+__device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// Four consecutive output columns col..col+3 of token row m (col % 4 == 0).
+template <int EPI>
+__device__ __forceinline__ void store4(bf16_t* y, int ldy, int m, int col, const f32x4_t& v) {
+    if constexpr (EPI == Q3_EPI_SWIGLU) {
+        const uint32_t lo = f2bf(silu_bf16(rbf(v[0])) * rbf(v[1]));
+        const uint32_t hi = f2bf(silu_bf16(rbf(v[2])) * rbf(v[3]));
+        *reinterpret_cast<uint32_t*>(y + (int64_t)m * ldy + (col >> 1)) = pack2(lo, hi);
+    } else {
+        uint2* p = reinterpret_cast<uint2*>(y + (int64_t)m * ldy + col);
+        if constexpr (EPI == Q3_EPI_RESID) {
+            const uint2 r = *p;
+            const uint32_t e0 = f2bf(bflo(r.x) + rbf(v[0])), e1 = f2bf(bfhi(r.x) + rbf(v[1]));
+            const uint32_t e2 = f2bf(bflo(r.y) + rbf(v[2])), e3 = f2bf(bfhi(r.y) + rbf(v[3]));
+            *p = make_uint2(pack2(e0, e1), pack2(e2, e3));
+        } else {
+            *p = make_uint2(pack2(f2bf(v[0]), f2bf(v[1])), pack2(f2bf(v[2]), f2bf(v[3])));
+        }
+    }
+}
+
+// ------------------------------------------------------------------ wide
+
+constexpr int WIDE_THREADS = 512;
+constexpr int WIDE_BK = 64;
+constexpr int WIDE_CPR = 8;                          // 16-byte chunks per 128-byte tile row
+constexpr int WIDE_TCH = 256 * WIDE_CPR;             // chunks per operand tile
+constexpr int WIDE_STAGE = 2 * WIDE_TCH * 16;        // 64 KB: W tile, then x tile
+constexpr int WIDE_DPT = WIDE_TCH / WIDE_THREADS;    // direct loads per operand per thread per step
+constexpr int WIDE_GROUP = 4;                        // token tiles per raster group
+
+// Position of 16-byte chunk c of 128-byte row r: c ^ ((r >> 1) & 7).  Measured
+// on gfx950: a ds_read_b128 whose 64 lanes read rows r0..r0+15 at one logical
+// chunk (four k groups) runs at the linear-read rate; no swizzle is 2.5x slower.
+__device__ __forceinline__ int wide_swz(int r) { return (r >> 1) & 7; }
+
+template <int EPI>
+__global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t* __restrict__ x, int ldx,
+                                                                    const bf16_t* __restrict__ w, int M, int N,
+                                                                    int K, bf16_t* __restrict__ y, int ldy, int tm,
+                                                                    int tn) {
+    __shared__ __align__(1024) char lds[2 * WIDE_STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int wn = wave & 3, wm = wave >> 2;  // sub-tile: weight rows 64wn.., tokens 128wm..
+
+    // Tile order: XCD-contiguous ranges, then groups of WIDE_GROUP token tiles
+    // sweeping the weight tiles.
+    const int tiles = tm * tn;
+    int t = blockIdx.x;
+    if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+    const int per_group = WIDE_GROUP * tn;
+    const int grp = t / per_group, first_m = grp * WIDE_GROUP;
+    const int gsz = min(WIDE_GROUP, tm - first_m);
+    const int in_g = t - grp * per_group;
+    const int m0 = (first_m + in_g % gsz) * 256, n0 = (in_g / gsz) * 256;
+
+    // Direct load j of thread tid fills chunk j*512 + tid of an operand tile:
+    // row 64j + tid/8, position tid%8 (wide_swz(r0 + 64j) == wide_swz(r0)).
+    // Rows past M or N re-read the last row: in bounds, results not stored.
+    const int r0 = tid >> 3;
+    const int c0 = (tid & 7) ^ wide_swz(r0);
+    const char* wbase = reinterpret_cast<const char*>(w + (int64_t)n0 * K);
+    const char* xbase = reinterpret_cast<const char*>(x + (int64_t)m0 * ldx);
+    uint32_t woff[WIDE_DPT], xoff[WIDE_DPT];
+#pragma unroll
+    for (int j = 0; j < WIDE_DPT; ++j) {
+        woff[j] = (uint32_t)((min(n0 + r0 + 64 * j, N - 1) - n0) * K + 8 * c0) * 2u;
+        xoff[j] = (uint32_t)((min(m0 + r0 + 64 * j, M - 1) - m0) * ldx + 8 * c0) * 2u;
+    }
+    const uint32_t lds_wave = lds_address(lds) + wave * 64 * 16;
+    auto issue = [&](int stage, int k0) {
+        const uint32_t base = lds_wave + stage * WIDE_STAGE;
+        const char* wb = wbase + 2 * k0;
+        const char* xb = xbase + 2 * k0;
+#pragma unroll
+        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(wb, woff[j], base + j * WIDE_THREADS * 16);
+#pragma unroll
+        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(xb, xoff[j], base + WIDE_TCH * 16 + j * WIDE_THREADS * 16);
+    };
+
+    f32x4_t acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Fragment i of a k half kk: rows 16i + n (same swizzle as row n), logical
+    // chunk 4kk + g.
+    const int ra = wn * 64 + n, rb = wm * 128 + n;
+    int aoff[2], boff[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        aoff[kk] = (ra * WIDE_CPR + ((4 * kk + g) ^ wide_swz(ra))) * 16;
+        boff[kk] = WIDE_TCH * 16 + (rb * WIDE_CPR + ((4 * kk + g) ^ wide_swz(rb))) * 16;
+    }
+    auto load_frags = [&](int stage, int kk, u32x4_t (&a)[4], u32x4_t (&b)[8]) {
+        const char* st = lds + stage * WIDE_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(st + aoff[kk] + i * 16 * 128);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(st + boff[kk] + j * 16 * 128);
+    };
+    auto mfmas = [&](const u32x4_t (&a)[4], const u32x4_t (&b)[8]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
+        // One LDS read, two MFMAs, twelve times, then the last eight MFMAs; the
+        // scheduler would otherwise sink the reads below the MFMAs.
+#pragma unroll
+        for (int q = 0; q < 12; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = K / WIDE_BK;
+    issue(0, 0);
+    issue(1, min(1, nk - 1) * WIDE_BK);
+    wait_vmcnt<2 * WIDE_DPT>();  // stage 0 landed (stage 1 may be in flight)
+    __syncthreads();
+    u32x4_t a0[4], b0[8], a1[4], b1[8];
+    load_frags(0, 0, a0, b0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int st = kt & 1;
+        load_frags(st, 1, a1, b1);
+        mfmas(a0, b0);
+        wait_vmcnt<0>();  // step kt+1 landed: the only direct loads in flight
+        __syncthreads();
+        // Stage kt is read no more: refill it with step kt+2.  Past the end the
+        // last K slice is loaded again (in bounds, never used), which keeps
+        // every wait count above fixed.
+        issue(st, min(kt + 2, nk - 1) * WIDE_BK);
+        load_frags(st ^ 1, 0, a0, b0);
+        mfmas(a1, b1);
+    }
+    wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
+
+    // acc[i][j][e] = C[token m0 + 128wm + 16j + n][column n0 + 64wn + 16i + 4g + e].
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int m = m0 + wm * 128 + 16 * j + n;
+        if (m >= M) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int col = n0 + wn * 64 + 16 * i + 4 * g;
+            if (col < N) store4<EPI>(y, ldy, m, col, acc[i][j]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- narrow
 
 constexpr int THREADS = 256;
 constexpr int BK = 64;
@@ -78,11 +288,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(const bf16_t* __restrict_
         }
     };
 
-    f32x4_t acc[FM][FN];
+    f32x4_t acc[FN][FM];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FM; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     gload(0);
     for (int k0 = 0; k0 < K; k0 += BK) {
@@ -92,47 +302,35 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(const bf16_t* __restrict_
         if (k0 + BK < K) gload(k0 + BK);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            bf16x8_t av[FM], bv[FN];
+            u32x4_t av[FN], bv[FM];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * TM + 16 * i + n;
-                av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(xs + r * BK + sw(r, 4 * kk + g) * 8));
+            for (int i = 0; i < FN; ++i) {
+                const int r = wn * TN + 16 * i + n;
+                av[i] = *reinterpret_cast<const u32x4_t*>(ws + r * BK + sw(r, 4 * kk + g) * 8);
             }
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int r = wn * TN + 16 * j + n;
-                bv[j] = as_bf16x8(*reinterpret_cast<const uint4*>(ws + r * BK + sw(r, 4 * kk + g) * 8));
+            for (int j = 0; j < FM; ++j) {
+                const int r = wm * TM + 16 * j + n;
+                bv[j] = *reinterpret_cast<const u32x4_t*>(xs + r * BK + sw(r, 4 * kk + g) * 8);
             }
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FN; ++i)
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FM; ++j) acc[i][j] = mfma(av[i], bv[j], acc[i][j]);
         }
     }
 
+    // acc[i][j][e] = C[token m0 + TM*wm + 16j + n][column n0 + TN*wn + 16i + 4g + e].
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FM; ++j) {
+        const int m = m0 + wm * TM + 16 * j + n;
+        if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * TN + 16 * j + n;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = m0 + wm * TM + 16 * i + 4 * g + e;
-                const float v = acc[i][j][e];
-                if constexpr (EPI == Q3_EPI_SWIGLU) {
-                    const float up = __shfl_xor(v, 1, Q3_WAVE);
-                    if ((col & 1) == 0 && row < M && col < N)
-                        y[(int64_t)row * ldy + (col >> 1)] = (bf16_t)f2bf(silu_bf16(rbf(v)) * rbf(up));
-                } else {
-                    if (row < M && col < N) {
-                        bf16_t* p = y + (int64_t)row * ldy + col;
-                        if constexpr (EPI == Q3_EPI_RESID) *p = (bf16_t)f2bf(bf2f(*p) + rbf(v));
-                        else *p = (bf16_t)f2bf(v);
-                    }
-                }
-            }
+        for (int i = 0; i < FN; ++i) {
+            const int col = n0 + wn * TN + 16 * i + 4 * g;
+            if (col < N) store4<EPI>(y, ldy, m, col, acc[i][j]);
         }
+    }
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -141,16 +339,39 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     switch (epi) {
         case Q3_EPI_STORE:
-            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_STORE>), grid, dim3(THREADS), 0, stream, x,
-                               ldx, w, M, N, K, y, ldy);
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_STORE>), grid, dim3(THREADS), 0, stream, x, ldx, w, M, N,
+                      K, y, ldy);
             break;
         case Q3_EPI_RESID:
-            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_RESID>), grid, dim3(THREADS), 0, stream, x,
-                               ldx, w, M, N, K, y, ldy);
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_RESID>), grid, dim3(THREADS), 0, stream, x, ldx, w, M, N,
+                      K, y, ldy);
             break;
         case Q3_EPI_SWIGLU:
-            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_SWIGLU>), grid, dim3(THREADS), 0, stream, x,
-                               ldx, w, M, N, K, y, ldy);
+            Q3_LAUNCH((gemm_kernel<BM, BN, WM, WN, Q3_EPI_SWIGLU>), grid, dim3(THREADS), 0, stream, x, ldx, w, M, N,
+                      K, y, ldy);
+            break;
+        default:
+            return (int)hipErrorInvalidValue;
+    }
+    Q3_CHECK_LAUNCH();
+}
+
+int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y, int ldy,
+                hipStream_t stream) {
+    const int tm = (M + 255) / 256, tn = (N + 255) / 256;
+    const dim3 grid(tm * tn);
+    switch (epi) {
+        case Q3_EPI_STORE:
+            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_STORE>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
+                      ldy, tm, tn);
+            break;
+        case Q3_EPI_RESID:
+            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_RESID>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
+                      ldy, tm, tn);
+            break;
+        case Q3_EPI_SWIGLU:
+            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_SWIGLU>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
+                      ldy, tm, tn);
             break;
         default:
             return (int)hipErrorInvalidValue;
@@ -160,12 +381,26 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
 
 }  // namespace
 
+// The wide tiling once it has at least this many 256 x 256 tiles (with fewer,
+// too many CUs would idle; measured on MI355X the 128 x 128 tiling is then
+// faster).
+constexpr int WIDE_MIN_TILES = 160;
+
+extern "C" int q3_gemm_tiles_wide(int M, int N) {
+    if (M < 1 || N < 1) return 0;
+    const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    return tiles >= WIDE_MIN_TILES && tiles <= (1 << 30);
+}
+
 extern "C" int q3_gemm(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
                        int ldy, hipStream_t stream) {
-    if (M < 1 || N < 1 || K < BK || K % BK || ldx % 8 || !x || !w || !y ||
-        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15))
+    if (M < 1 || N < 4 || N % 4 || K < BK || K % BK || ldx % 8 || ldx < K || ldy % 4 || !x || !w || !y ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) ||
+        (reinterpret_cast<uintptr_t>(y) & 7))
         return (int)hipErrorInvalidValue;
-    if (epi == Q3_EPI_SWIGLU && (N % 2)) return (int)hipErrorInvalidValue;
+    // A token tile's rows lie within 32-bit byte offsets of its first row.
+    if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
+    if (q3_gemm_tiles_wide(M, N)) return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 16) return launch<16, 64, 1, 4>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 32) return launch<32, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 64) return launch<64, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);

@@ -441,3 +441,41 @@ extern "C" int q3_argmax_rows(const bf16_t* logits, int ld, int B, int V, int64_
     Q3_LAUNCH(argmax_rows_kernel, dim3(B), dim3(THREADS), 0, stream, logits, ld, V, B, tokens, pos, counter, sr);
     Q3_CHECK_LAUNCH();
 }
+
+// ------------------------------------------------------------------ SwiGLU
+
+namespace {
+
+// out[r, j] = bf16(bf16(silu(g)) * u) with (g, u) = gu[r, 2j], gu[r, 2j + 1]
+// (gate/up rows interleaved, as the decode epilogue reads them).  Eight
+// outputs per thread: two 16-byte loads, one 16-byte store.
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const bf16_t* __restrict__ gu, bf16_t* __restrict__ out,
+                                                          int64_t chunks, int ichunks) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const int64_t r = c / ichunks, j = c % ichunks;
+    const bf16_t* src = gu + (r * ichunks + j) * 16;
+    const uint4 p0 = *reinterpret_cast<const uint4*>(src);
+    const uint4 p1 = *reinterpret_cast<const uint4*>(src + 8);
+    const uint32_t w[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = f2bf(silu_bf16(bflo(w[2 * k])) * bfhi(w[2 * k]));
+        const uint32_t hi = f2bf(silu_bf16(bflo(w[2 * k + 1])) * bfhi(w[2 * k + 1]));
+        o[k] = pack2(lo, hi);
+    }
+    *reinterpret_cast<uint4*>(out + (r * ichunks + j) * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace
+
+extern "C" int q3_swiglu_rows(const bf16_t* gu, bf16_t* out, int rows, int I, hipStream_t stream) {
+    if (rows < 1 || I < 8 || I % 8 || !gu || !out ||
+        ((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(out)) & 15))
+        return (int)hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)rows * (I / 8);
+    Q3_LAUNCH(swiglu_rows_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, gu, out, chunks,
+              I / 8);
+    Q3_CHECK_LAUNCH();
+}

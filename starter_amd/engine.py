@@ -77,12 +77,6 @@ MEMORY_MARGIN_BYTES = 2 << 30
 GEMV_BATCH_MAX = 4
 SKINNY_BATCH_MAX = 64
 
-#: Prompt-pass projections through hipBLASLt (``q3_gemm_lt``), with the residual
-#: join in the add+norm kernel and SwiGLU as a row kernel; False keeps the
-#: library's own MFMA GEMM with fused epilogues.
-PREFILL_BLASLT = os.environ.get("Q3_PREFILL_BLASLT", "1") != "0"
-LT_WORKSPACE_BYTES = 64 << 20
-
 #: Decode attention and its split merge in one launch where the grid allows it
 #: (``q3_attn_decode_fused``); False keeps two launches (tests compare them).
 FUSED_ATTENTION = os.environ.get("Q3_FUSED_ATTENTION", "1") != "0"
@@ -207,7 +201,6 @@ class Engine:
         self.graph = None
         self.keep_logits = False
         self._prefill_bufs = {}
-        self.lt_ws = None  # hipBLASLt workspace, made with the first prompt-pass buffers
         _log(f"loaded {self.LAYERS} layers in {time.monotonic() - self.started:.1f}s; "
              f"qkv and gate_up packed")
 
@@ -547,15 +540,7 @@ class Engine:
                 "act": self._empty(rows, self.INTER),
             }
             self._prefill_bufs[rows] = bufs
-        if PREFILL_BLASLT and "gu" not in bufs:
-            bufs["t"] = self._empty(rows, self.HIDDEN)
-            bufs["gu"] = self._empty(rows, 2 * self.INTER)
-            if self.lt_ws is None:
-                self.lt_ws = torch.empty(LT_WORKSPACE_BYTES, dtype=torch.uint8, device=self.device)
         return bufs
-
-    def _gemm_lt(self, x: int, ldx: int, w: torch.Tensor, M: int, N: int, K: int, y: int, ldy: int) -> None:
-        call("q3_gemm_lt", x, ldx, _ptr(w), M, N, K, y, ldy, _ptr(self.lt_ws), LT_WORKSPACE_BYTES, self._s)
 
     def _forward_prefill(self, ids: torch.Tensor, seq_len: int) -> torch.Tensor:
         """Consume the prompt ``ids [B, P]``; return the last position's logits [B, 1, V].
@@ -591,35 +576,21 @@ class Engine:
                 bufs = self._prefill_buffers(B * min(chunk, seq_len))
                 chunk_ids = ids[:, start:stop].contiguous()
                 resid, n, qkv, q, a, act = (_ptr(bufs[k]) for k in ("resid", "n", "qkv", "q", "a", "act"))
-                lt = PREFILL_BLASLT
                 for i, L in enumerate(self.layers):
                     if i == 0:
                         call("q3_embed_rmsnorm", _ptr(chunk_ids), _ptr(self.embed), resid, n,
                              _ptr(L["in_ln"]), M, H, self.EPS, s)
-                    elif not lt:
-                        call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), n, H, M, H, self.EPS, s)
-                    if lt:
-                        self._gemm_lt(n, H, L["qkv"], M, self.qkv_size, H, qkv, self.qkv_size)
                     else:
-                        call("q3_gemm", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
-                             self.qkv_size, s)
+                        call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), n, H, M, H, self.EPS, s)
+                    call("q3_gemm", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
+                         self.qkv_size, s)
                     call("q3_qk_norm_rope_kv", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                          _ptr(self.cos_table), _ptr(self.sin_table), None, start, q,
                          kc0 + i * layer_stride, vc0 + i * layer_stride, B, T, Hq, Hkv, D, C, self.EPS, s)
                     call("q3_attn_prefill", q, kc0 + i * layer_stride, vc0 + i * layer_stride, a, B, T,
                          start, Hq, Hkv, C, self.SCALE, s)
-                    if lt:
-                        # Same rounding points as the fused epilogues: resid = bf16(resid +
-                        # bf16(acc)) then the next norm; act = bf16(bf16(silu(g)) * u).
-                        t, gu = _ptr(bufs["t"]), _ptr(bufs["gu"])
-                        nxt = self.layers[i + 1]["in_ln"] if i + 1 < len(self.layers) else self.final_norm
-                        self._gemm_lt(a, self.q_size, L["o"], M, H, self.q_size, t, H)
-                        call("q3_add_rmsnorm", resid, t, resid, n, _ptr(L["post_ln"]), M, H, self.EPS, s)
-                        self._gemm_lt(n, H, L["gate_up"], M, 2 * I, H, gu, 2 * I)
-                        call("q3_swiglu_rows", gu, act, M, I, s)
-                        self._gemm_lt(act, I, L["down"], M, H, I, t, H)
-                        call("q3_add_rmsnorm", resid, t, resid, n, _ptr(nxt), M, H, self.EPS, s)
-                        continue
+                    # Residual join and SwiGLU in the GEMM epilogues, at the reference's
+                    # rounding points: resid = bf16(resid + bf16(acc)); act = bf16(bf16(silu(g)) * u).
                     call("q3_gemm", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
                          resid, H, s)
                     call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), n, H, M, H, self.EPS, s)

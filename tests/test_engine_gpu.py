@@ -88,27 +88,21 @@ def test_prefill_logit_delta(tiny_engine):
     assert delta < min(TOL_TINY, 0.05 * max(np.abs(want).max(), 1.0)), delta
 
 
-def test_prefill_paths_agree(tiny_engine):
-    """The prompt pass with hipBLASLt projections (default) and with the library's
-    own MFMA GEMM and fused epilogues: both within TOL of HF's prefill logits and
-    of each other (they differ only in the projections' summation order)."""
+def test_prefill_repeatable(tiny_engine):
+    """The prompt pass (own MFMA GEMMs with fused residual and SwiGLU epilogues)
+    is within TOL of HF's prefill logits and bit-identical on a repeat, with
+    the result read on the caller's stream without an explicit sync of the
+    engine's stream (the engine orders the caller's stream after its own)."""
     g = golden("tiny_bf16")
     ids = torch.from_numpy(g["prefill/ids"])
     want = g["prefill/logits"]
-    saved = engine_mod.PREFILL_BLASLT
     outs = []
-    try:
-        for lt in (True, False, True):
-            engine_mod.PREFILL_BLASLT = lt
-            tiny_engine._ensure_shape(2, 40, 4)
-            # No sync on the engine's stream: the result is read on the caller's.
-            outs.append(tiny_engine._forward_prefill(ids, 40).float().cpu()[:, 0])
-    finally:
-        engine_mod.PREFILL_BLASLT = saved
+    for _ in range(2):
+        tiny_engine._ensure_shape(2, 40, 4)
+        outs.append(tiny_engine._forward_prefill(ids, 40).float().cpu()[:, 0])
     for o in outs:
         assert np.abs(o.numpy() - want).max() < TOL_TINY
-    assert (outs[0] - outs[1]).abs().max() <= TOL_TINY
-    assert torch.equal(outs[0], outs[2])  # each path is deterministic, and switching back restores it
+    assert torch.equal(outs[0], outs[1])
 
 
 def test_yield_contract(tiny_engine):

@@ -355,28 +355,59 @@ def test_gemm(M, N, K):
     assert_nearly_exact(act, oc.swiglu(yc[:, 0::2], yc[:, 1::2]), frac=5e-3)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 320, 1024), (300, 1536, 320), (513, 2560, 2560), (2048, 6144, 2560),
-                                   (1000, 2560, 9728)])
-def test_gemm_lt(M, N, K):
-    """Prompt-pass projection through hipBLASLt: the float64 dot products of the
-    same BF16 operands, rounded once (the same bar as the MFMA GEMM), with a
-    row stride on x and y."""
-    x, w = rnd((M, K + 64), 1.0, M + 3)[:, :K], rnd((N, K), 0.02, N + K + 3)
-    xd, wd = dv(x.contiguous()), dv(w)
-    xs = dv(torch.zeros(M, K + 64, dtype=torch.bfloat16))
-    xs[:, :K] = xd
-    y = dv(torch.full((M, N + 8), 7.0, dtype=torch.bfloat16))
-    ws = dv(torch.empty(64 << 20, dtype=torch.uint8))
-    call("q3_gemm_lt", P(xs), K + 64, P(wd), M, N, K, P(y), N + 8, P(ws), 64 << 20, S())
+@pytest.mark.parametrize("M,N,K,epi", [(4096, 6144, 2560, _lib.EPI_STORE), (4096, 2560, 4096, _lib.EPI_RESID),
+                                       (2600, 19456, 2560, _lib.EPI_SWIGLU), (4096, 2560, 9728, _lib.EPI_RESID),
+                                       (3000, 3800, 320, _lib.EPI_STORE), (40961, 4096, 64, _lib.EPI_STORE)])
+def test_gemm_wide(M, N, K, epi):
+    """The 256 x 256-tile path at the prompt pass's projection shapes, plus ragged
+    token and weight tiles (M % 256, N % 256 != 0; an odd K step count; one K
+    step): every epilogue checked on 96 sampled token rows (first, last, and
+    random) against float64 dot products of the same BF16 operands, and the
+    columns past N / rows past M of the output buffer untouched."""
+    assert call("q3_gemm_tiles_wide", M, N) == 1
+    g = torch.Generator().manual_seed(M + N + K)
+    x, w = rnd((M, K), 1.0, M + 7), rnd((N, K), 0.02, N + K + 7)
+    xd, wd = dv(x), dv(w)
+    cols = N // 2 if epi == _lib.EPI_SWIGLU else N
+    res = rnd((M, cols), 1.0, 9) if epi == _lib.EPI_RESID else torch.full((M, cols), 7.0, dtype=torch.bfloat16)
+    pad = dv(torch.full((M + 1, cols + 4), 5.0, dtype=torch.bfloat16))
+    pad[:M, :cols] = dv(res)
+    call("q3_gemm", P(xd), K, P(wd), M, N, K, epi, P(pad), cols + 4, S())
     torch.cuda.synchronize()
-    check_projection(y[:, :N], x, w)
-    assert torch.all(y[:, N:].cpu() == 7.0)  # the row padding is not written
+    out = pad.cpu()
+    assert torch.all(out[:, cols:] == 5.0) and torch.all(out[M] == 5.0)
+    rows = torch.cat([torch.tensor([0, M - 1]), torch.randint(0, M, (94,), generator=g)])
+    xs = x[rows]
+    if epi == _lib.EPI_STORE:
+        check_projection(out[rows, :N], xs, w)
+        return
+    # The fused epilogues against the unfused ones on the same rows: the plain
+    # projection of those rows (checked above for its own bar) is recomputed
+    # here through the narrow tiling, whose sums the wide path must match to
+    # the same float64 bar.
+    y = torch.empty(len(rows), N, dtype=torch.bfloat16, device=DEV)
+    call("q3_gemm", P(dv(xs.contiguous())), K, P(wd), len(rows), N, K, _lib.EPI_STORE, P(y), N, S())
+    torch.cuda.synchronize()
+    yc = y.cpu()
+    check_projection(yc, xs, w)
+    if epi == _lib.EPI_RESID:
+        want = (res[rows].float() + yc.float()).bfloat16()
+        got = out[rows, :N]
+        # Both round once from FP32 sums of different order: at most one BF16
+        # ulp of the projection apart, on a small fraction of elements.
+        diff = (got.float() - want.float()).abs()
+        assert (diff > 0).float().mean() <= 0.03
+        assert torch.all(diff <= 2.0 ** -7 * (want.float().abs() + yc.float().abs()) + 1e-6)
+    else:
+        want = oc.swiglu(yc[:, 0::2], yc[:, 1::2])
+        assert_nearly_exact(out[rows, :cols], want, frac=0.06, max_ulp=2)
 
 
-@pytest.mark.parametrize("rows,I", [(1, 8), (7, 1024), (300, 9728)])
+@pytest.mark.parametrize("rows,I", [(1, 8), (7, 1024), (300, 9728), (640, 9728)])
 def test_swiglu_rows_matches_fused_epilogue(rows, I):
     """q3_swiglu_rows on a stored gate/up projection == the GEMM's fused SwiGLU
-    epilogue, bit for bit (both round the accumulator to BF16 first)."""
+    epilogue, bit for bit (both round the accumulator to BF16 first); 640 rows
+    take the 256 x 256-tile path."""
     K = 256
     x, w = rnd((rows, K), 1.0, rows + 11), rnd((2 * I, K), 0.05, I + 12)
     xd, wd = dv(x), dv(w)
