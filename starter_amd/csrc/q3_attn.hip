@@ -19,8 +19,12 @@
 // pairing of operands is what matters.
 #include "q3_attn_mfma.hpp"
 #include "q3_common.hpp"
+#include "q3_dma.hpp"
 #include "q3_exchange.hpp"
 #include "q3.h"
+
+// q3dma::load_to_lds clobbers m0, which nothing else in this file uses.
+#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace {
 
@@ -35,28 +39,6 @@ constexpr int THREADS = 256; // 4 waves
 // 16 bytes.
 constexpr int XREC = 2 * 128 + 4 + 4;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-
-// LDS V tile of the prefill kernel [32 keys][128 d] BF16, 16-byte chunks
-// swizzled so the column reads for keys kappa(g, t) hit four distinct bank groups.
-__device__ __forceinline__ int v_chunk(int key, int c) { return c ^ (((key >> 2) & 3) << 2); }
-// LDS K tile of the prefill kernel [32 keys][128 d]: rows read 16 at a time at one chunk.
-__device__ __forceinline__ int k_chunk(int key, int c) { return c ^ (key & 15); }
-
-__device__ __forceinline__ int kappa(int g, int t) { return t < 4 ? 4 * g + t : 16 + 4 * g + (t - 4); }
-
-// A operand of the P.V MFMA for d block dm: V^T[d = 16dm + n][kappa(g, t)].
-__device__ __forceinline__ bf16x8_t vt_operand(const bf16_t* vs, int dm, int n, int g) {
-    const int d = 16 * dm + n;
-    const int c = d >> 3, e = d & 7;
-    uint32_t h[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int key = kappa(g, t);
-        h[t] = vs[key * D + v_chunk(key, c) * 8 + e];
-    }
-    uint4 v = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
-    return as_bf16x8(v);
-}
 
 // Per-head RMSNorm + RoPE of one 128-wide row held as (lo = x[l], hi = x[l+64])
 // in lane l (reference fused.py:161-219): returns bf16 bits of both halves.
@@ -566,23 +548,32 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const float* part_acc, co
 
 // ----------------------------------------------------------------- prefill
 
+constexpr int PBLK = 64;                   // keys per prefill block
+constexpr int PTILE = PBLK * D * 2;        // bytes of one K (or V) block tile
+constexpr int PSTAGE = 2 * PTILE;          // K tile then V tile
+constexpr int PDMA = PBLK * 16 / THREADS;  // direct loads per tile per thread (4)
+
 // grid (ceil(T/32), Hkv, B); wave w = query head kvh*4 + w, 32 queries per
-// workgroup (two MFMA column blocks of 16).  K and V blocks of 32 keys are
-// staged in LDS once and shared by the four heads; the next block's rows are
-// loaded into registers while the current one computes.  Workgroups start
-// with the last queries (the longest causal ranges), so the short ones fill
-// the tail of the launch.
+// workgroup (two MFMA column blocks of 16).  Keys advance 64 at a time through
+// two LDS stages (K and V tiles in the decode layout, kv_slot) filled by
+// direct global-to-LDS loads, so the four heads share each K/V byte and the
+// next block streams in while this one computes.  Per block and column block:
+// S^T = K.Q^T (16 MFMAs), the online softmax in base 2 (scores scaled by
+// scale*log2(e) inside one FMA; the causal mask only on blocks that cross the
+// diagonal of some query), P rounded to BF16 by v_cvt_pk_bf16_f32, and
+// O^T += V^T.P^T (16 MFMAs, V^T through transposing LDS reads).  Workgroups
+// start with the last queries (the longest causal ranges), so the short ones
+// fill the tail of the launch.
 __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* q, const bf16_t* cache_k,
                                                                const bf16_t* cache_v, bf16_t* out,
                                                                int T, int start, int Hq, int Hkv,
                                                                int capacity, float scale) {
+    __shared__ __align__(1024) char lds[2 * PSTAGE];
     const int qb0 = (gridDim.x - 1 - blockIdx.x) * 32, kvh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int h = kvh * GROUP + w;
-
-    __shared__ __align__(16) bf16_t ks[BLK * D];
-    __shared__ __align__(16) bf16_t vs[BLK * D];
 
     // Q^T operands for the two 16-query column blocks.
     bf16x8_t qb[2][4];
@@ -598,9 +589,31 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
         }
     }
 
-    const bf16_t* kbase = cache_k + ((int64_t)b * Hkv + kvh) * capacity * D;
-    const bf16_t* vbase = cache_v + ((int64_t)b * Hkv + kvh) * capacity * D;
+    const int q_last = min(qb0 + 31, T - 1);
+    const int key_end = start + q_last + 1;  // keys 0 .. start+q_last
+    const int nblk = (key_end + PBLK - 1) / PBLK;
+    const int full_end = start + qb0 + 1;    // keys below it are visible to every query here
 
+    // Direct load j of thread tid fills 16-byte slot 256j + tid of a tile:
+    // key 16j + tid/16, slot position tid%16, i.e. chunk (tid%16) ^ (key & 15)
+    // (kv_slot).  Keys past key_end re-read key_end - 1 (inside the cache);
+    // every query masks them, so they add exactly zero.
+    const char* kbase = reinterpret_cast<const char*>(cache_k + ((int64_t)b * Hkv + kvh) * capacity * D);
+    const char* vbase = reinterpret_cast<const char*>(cache_v + ((int64_t)b * Hkv + kvh) * capacity * D);
+    const int krow = tid >> 4, kchunk = (tid & 15) ^ (krow & 15);
+    const uint32_t lds_thr = q3dma::lds_address(lds) + w * 64 * 16;
+    auto issue = [&](int stage, int kb) {
+        const uint32_t base = lds_thr + stage * PSTAGE;
+#pragma unroll
+        for (int j = 0; j < PDMA; ++j) {
+            const int key = min(kb + 16 * j + krow, key_end - 1);
+            const uint32_t voff = (uint32_t)(key * D + 8 * kchunk) * 2u;
+            q3dma::load_to_lds(kbase, voff, base + j * THREADS * 16);
+            q3dma::load_to_lds(vbase, voff, base + PTILE + j * THREADS * 16);
+        }
+    };
+
+    const float c = scale * 1.4426950408889634f;  // scores in base-2 units
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
     f32x4_t acc[2][8];
 #pragma unroll
@@ -608,78 +621,89 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
 #pragma unroll
         for (int dm = 0; dm < 8; ++dm) acc[cb][dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int q_last = min(qb0 + 31, T - 1);
-    const int key_end = start + q_last + 1;  // keys 0 .. start+q_last
-    // 32 keys x 256 B for K and V: 512 16-byte chunks each, 2 per thread.
-    // Rows past key_end re-read key_end - 1 (inside the cache); every query
-    // of the workgroup masks them, so they add exactly zero.
-    u32x4_t kr[2], vr[2];
-    auto load_block = [&](int kb) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int e = tid + j * THREADS;
-            const int key = min(kb + (e >> 4), key_end - 1), c = e & 15;
-            kr[j] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + 8 * c);
-            vr[j] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + 8 * c);
-        }
-    };
-    load_block(0);
-    for (int kb = 0; kb < key_end; kb += BLK) {
+    issue(0, 0);
+    issue(1, min(1, nblk - 1) * PBLK);
+    for (int blk = 0; blk < nblk; ++blk) {
+        const int kb = blk * PBLK, st = blk & 1;
+        q3dma::wait_vmcnt<2 * PDMA>();  // this block landed; the next one may be in flight
         __syncthreads();
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int e = tid + j * THREADS;
-            const int r = e >> 4, c = e & 15;
-            *reinterpret_cast<u32x4_t*>(ks + r * D + k_chunk(r, c) * 8) = kr[j];
-            *reinterpret_cast<u32x4_t*>(vs + r * D + v_chunk(r, c) * 8) = vr[j];
-        }
-        __syncthreads();
-        // The next block (the last one again on the final pass: rows clamp)
-        // streams in while this one computes.
-        load_block(min(kb + BLK, key_end - 1));
-        __builtin_amdgcn_sched_barrier(0);
+        const bf16_t* kt = reinterpret_cast<const bf16_t*>(lds + st * PSTAGE);
+        const bf16_t* vt = kt + PTILE / 2;
 
-        bf16x8_t kop[2][4];
+        f32x4_t s[2][4];
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            const int r = 16 * hb + n;
+        for (int hb = 0; hb < 4; ++hb) {
+            const int key = 16 * hb + n;
+            s[0][hb] = s[1][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                kop[hb][kk] = as_bf16x8(*reinterpret_cast<const uint4*>(ks + r * D + k_chunk(r, 4 * g + kk) * 8));
+            for (int kk = 0; kk < 4; ++kk) {
+                // k slot (g, t) is d = 32g + 8kk + t on both operands (qb's layout).
+                const bf16x8_t kf = __builtin_bit_cast(
+                    bf16x8_t, reinterpret_cast<const u32x4_t*>(kt)[kv_slot(key, 4 * g + kk)]);
+                s[0][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[0][kk], s[0][hb], 0, 0, 0);
+                s[1][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[1][kk], s[1][hb], 0, 0, 0);
+            }
         }
-        bf16x8_t pb[2];
+        const bool masked = kb + PBLK > full_end;  // some key here lies past some query
+        bf16x8_t pb[2][2];
         float alpha[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const int qpos = start + qb0 + 16 * cb + n;  // this lane's query position
-            f32x4_t s[2];
+            float mx = -INFINITY;
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                s[hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
-                    s[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[hb][kk], qb[cb][kk], s[hb], 0, 0, 0);
+                for (int i = 0; i < 4; ++i) {
+                    if (masked && kb + 16 * hb + 4 * g + i > qpos) s[cb][hb][i] = -INFINITY;
+                    mx = fmaxf(mx, s[cb][hb][i]);
+                }
+            const float m_new = fmaxf(m[cb], group_max(mx));  // key 0 is visible to every query: finite
+            alpha[cb] = __builtin_amdgcn_exp2f((m[cb] - m_new) * c);
+            const float mc = m_new * c;
+            float sum = 0.f;
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[cb][hb][i], c, -mc));
+                    s[cb][hb][i] = p;
+                    sum += p;
+                }
+            l[cb] = l[cb] * alpha[cb] + group_sum(sum);
+            m[cb] = m_new;
+            // P^T operand of k step j: keys 32j + 4g + t (t < 4), then 32j + 16 + 4g + t.
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                typedef float f32x2_t __attribute__((ext_vector_type(2)));
+                typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+                uint32_t u[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f32x4_t& src = s[cb][2 * j + (e >> 1)];
+                    const f32x2_t pair = {src[2 * (e & 1)], src[2 * (e & 1) + 1]};
+                    u[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2v_t));
+                }
+                pb[cb][j] = as_bf16x8(make_uint4(u[0], u[1], u[2], u[3]));
             }
-            float s0[4], s1[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int k0 = kb + 4 * g + i, k1 = kb + 16 + 4 * g + i;
-                s0[i] = (k0 <= qpos) ? s[0][i] * scale : -INFINITY;
-                s1[i] = (k1 <= qpos) ? s[1][i] * scale : -INFINITY;
-            }
-            alpha[cb] = softmax_block(s0, s1, m[cb], l[cb]);
-            pb[cb] = p_operand(s0, s1);
         }
 #pragma unroll
-        for (int dm = 0; dm < 8; ++dm) {
-            const bf16x8_t va = vt_operand(vs, dm, n, g);
+        for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                acc[cb][dm] *= alpha[cb];
-                acc[cb][dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb], acc[cb][dm], 0, 0, 0);
+            for (int dm = 0; dm < 8; ++dm) acc[cb][dm] *= alpha[cb];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dm = 0; dm < 8; ++dm) {
+                const bf16x8_t va = vt_operand_tr(vt + j * 32 * D, dm, lane);
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+                    acc[cb][dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][j], acc[cb][dm], 0, 0, 0);
             }
-        }
+        __syncthreads();  // every wave is done with this stage: refill it two blocks ahead
+        issue(st, min(blk + 2, nblk - 1) * PBLK);
     }
+    q3dma::wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -688,9 +712,11 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
             const float inv_l = 1.0f / l[cb];
             bf16_t* dst = out + (((int64_t)b * T + qi) * Hq + h) * D;
 #pragma unroll
-            for (int dm = 0; dm < 8; ++dm)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) dst[16 * dm + 4 * g + i] = (bf16_t)f2bf(acc[cb][dm][i] * inv_l);
+            for (int dm = 0; dm < 8; ++dm) {
+                const f32x4_t& a = acc[cb][dm];
+                *reinterpret_cast<uint2*>(dst + 16 * dm + 4 * g) =
+                    make_uint2(pack2(f2bf(a[0] * inv_l), f2bf(a[1] * inv_l)), pack2(f2bf(a[2] * inv_l), f2bf(a[3] * inv_l)));
+            }
         }
     }
 }
@@ -833,6 +859,8 @@ extern "C" int q3_attn_prefill(const bf16_t* q, const bf16_t* cache_k, const bf1
                                int B, int T, int start, int Hq, int Hkv, int capacity, float scale,
                                hipStream_t stream) {
     if (B < 1 || T < 1 || start < 0 || Hq != GROUP * Hkv || start + T > capacity) return (int)hipErrorInvalidValue;
+    // One (sequence, KV head) cache row block lies within 32-bit byte offsets.
+    if ((int64_t)capacity * D * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
     Q3_LAUNCH(attn_prefill_kernel, dim3((T + 31) / 32, Hkv, B), dim3(THREADS), 0, stream,
                        q, cache_k, cache_v, out, T, start, Hq, Hkv, capacity, scale);
     Q3_CHECK_LAUNCH();

@@ -30,40 +30,12 @@
 // consecutive output columns of one token row (8-byte stores; both halves of a
 // SwiGLU pair in one lane).
 #include "q3_common.hpp"
+#include "q3_dma.hpp"
 #include "q3.h"
 
 namespace {
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; expcnt
-// and lgkmcnt left at their maxima, so they are not waited for).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// 16 bytes per lane from sbase + voff straight into LDS at m0 + 16 * lane
-// (global_load_lds_dwordx4, scalar base + 32-bit lane offset).  Written as asm
-// because the compiler otherwise makes every later LDS read wait for all
-// direct-to-LDS loads in flight, which serialises the pipeline; the kernel
-// waits for exactly the stage it needs (vmcnt) and then takes a barrier.
-// Nothing else in these kernels uses m0 (clang warns that a clobbered m0 is
-// not restored for code that would).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void load_to_lds(const void* sbase, uint32_t voff, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0\n"
-                 :
-                 : "s"(sbase), "v"(voff), "s"(m0)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    return (uint32_t)reinterpret_cast<uintptr_t>((lds_ptr_t)p);
-}
+using namespace q3dma;
 
 __device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),

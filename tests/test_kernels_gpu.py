@@ -492,8 +492,12 @@ def test_attn_decode(B, C, pos, splits):
     assert (err <= 1e-2 + 1e-2 * want.abs()).all(), f"max err {err.max():.3e}"
 
 
-@pytest.mark.parametrize("B,T,start", [(1, 1, 0), (2, 37, 0), (1, 64, 0), (2, 20, 30), (3, 50, 13)])
+@pytest.mark.parametrize("B,T,start", [(1, 1, 0), (2, 37, 0), (1, 64, 0), (2, 20, 30), (3, 50, 13), (1, 300, 0),
+                                       (2, 130, 70), (1, 1000, 24), (1, 97, 4000)])
 def test_attn_prefill(B, T, start):
+    """Chunks at offset `start` over a cache of start + T + 5 slots: one and many
+    64-key blocks, blocks crossing the diagonal of some but not all queries, a
+    ragged last query block, and a long prefix with a short chunk."""
     Hq, Hkv, D = 32, 8, 128
     C = start + T + 5
     q = rnd((B * T, Hq, D), 1.0, T)
