@@ -355,11 +355,12 @@ int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, 
 
 // The wide tiling once it has at least this many 256 x 256 tiles (with fewer,
 // too many CUs would idle; measured on MI355X the 128 x 128 tiling is then
-// faster).
+// faster) and at least one full token tile (a 64-row LM head would waste
+// three quarters of each tile's MFMA work).
 constexpr int WIDE_MIN_TILES = 160;
 
 extern "C" int q3_gemm_tiles_wide(int M, int N) {
-    if (M < 1 || N < 1) return 0;
+    if (M < 256 || N < 1) return 0;
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
     return tiles >= WIDE_MIN_TILES && tiles <= (1 << 30);
 }
