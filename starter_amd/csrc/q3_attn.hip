@@ -590,6 +590,11 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
             qb[cb][kk] = as_bf16x8(v);
         }
     }
+    // Q in registers before any direct load is issued: otherwise the
+    // compiler's wait for Q at its first use inside the key loop (it cannot
+    // see the direct loads) is a vmcnt(0) that every block then executes,
+    // waiting for the next block's loads as well.
+    q3dma::wait_vmcnt<0>();
 
     const int q_last = min(qb0 + 31, T - 1);
     const int key_end = start + q_last + 1;  // keys 0 .. start+q_last

@@ -52,14 +52,23 @@ __device__ __forceinline__ bf16x8_t p_operand(const float p0[4], const float p1[
     return as_bf16x8(v);
 }
 
-// Max / sum over the four lane groups that hold one query's keys.
+// Max / sum over the four lane groups that hold one query's keys (lanes n,
+// n+16, n+32, n+48).  gfx950's cross-row swaps stay in the VALU (no LDS
+// round trip): v_permlane16_swap on (v, v) leaves each lane its own value and
+// that of lane l ^ 16 (the pair's order differs between even and odd rows,
+// which max and + do not see), v_permlane32_swap the same for l ^ 32.  The
+// sum is (v_l + v_l^16) + (v_l^32 + v_l^48), as a butterfly of shuffles gives.
 __device__ __forceinline__ float group_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, Q3_WAVE));
-    return fmaxf(v, __shfl_xor(v, 32, Q3_WAVE));
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float group_sum(float v) {
-    v += __shfl_xor(v, 16, Q3_WAVE);
-    return v + __shfl_xor(v, 32, Q3_WAVE);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Online-softmax update of one 32-key block for this lane's query.
