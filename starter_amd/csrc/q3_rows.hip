@@ -195,46 +195,72 @@ __global__ __launch_bounds__(THREADS) void add_rmsnorm_partials_kernel(const flo
     }
 }
 
-// Per (token, head) RMSNorm over 128 then RoPE (lane l holds d = l and l+64).
-__device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w, const bf16_t* cosr,
-                                               const bf16_t* sinr, float eps, int lane, bf16_t* dst) {
-    const float lo = bf2f(x[lane]), hi = bf2f(x[lane + 64]);
-    const float inv = inv_rms(wave_sum(lo * lo + hi * hi), 128, eps);
-    const float n_lo = bf2f(norm_elem(lo, inv, bf2f(w[lane])));
-    const float n_hi = bf2f(norm_elem(hi, inv, bf2f(w[lane + 64])));
-    const float c_lo = bf2f(cosr[lane]), s_lo = bf2f(sinr[lane]);
-    const float c_hi = bf2f(cosr[lane + 64]), s_hi = bf2f(sinr[lane + 64]);
-    dst[lane] = (bf16_t)f2bf(rbf(n_lo * c_lo) + rbf(-n_hi * s_lo));
-    dst[lane + 64] = (bf16_t)f2bf(rbf(n_hi * c_hi) + rbf(n_lo * s_hi));
-}
-
-// grid (B*T): one workgroup per token, waves stride over Hq q-heads, Hkv
-// k-heads and Hkv v-heads.
+// grid (B*T): one workgroup per token.  A 16-lane group takes one head: lane
+// i holds d = 8i .. 8i+7 (one 16-byte load of the head's 256 contiguous
+// bytes), so a wave covers four heads per pass and each token's row, RoPE rows
+// and gains are read once, whole.  Per head: RMSNorm over 128 (the 16 lanes'
+// sums of squares added by a butterfly, the same total in every lane), then
+// RoPE, whose partner of d (d -+ 64) sits in lane i ^ 8 of the group (one DPP
+// rotation by 8 within the 16-lane row).  Cast points as the reference's
+// (rmsnorm.py:34-45, fused.py:161-219): the normalised value rounds before the
+// gain, each RoPE product rounds before the sum.
 __global__ __launch_bounds__(THREADS) void qk_norm_rope_kv_kernel(
     const bf16_t* qkv, int ld_qkv, const bf16_t* qw, const bf16_t* kw, const bf16_t* cos_t,
     const bf16_t* sin_t, const int64_t* start_pos, int start_offset, bf16_t* q_out, bf16_t* cache_k,
     bf16_t* cache_v, int T, int Hq, int Hkv, int capacity, float eps) {
     const int bt = blockIdx.x, b = bt / T, t = bt % T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 4, i = lane & 15;
     const int pos = (start_pos ? (int)*start_pos : 0) + start_offset + t;
     if (pos < 0 || pos >= capacity) return;  // never write outside the cache
     const bf16_t* row = qkv + (int64_t)bt * ld_qkv;
-    const bf16_t* cosr = cos_t + (int64_t)pos * 128;
-    const bf16_t* sinr = sin_t + (int64_t)pos * 128;
-    for (int h = wave; h < Hq + 2 * Hkv; h += THREADS / 64) {
-        if (h < Hq) {
-            head_norm_rope(row + h * 128, qw, cosr, sinr, eps, lane, q_out + ((int64_t)bt * Hq + h) * 128);
-        } else if (h < Hq + Hkv) {
-            const int kh = h - Hq;
-            bf16_t* dst = cache_k + (((int64_t)b * Hkv + kh) * capacity + pos) * 128;
-            head_norm_rope(row + h * 128, kw, cosr, sinr, eps, lane, dst);
-        } else {
-            const int vh = h - Hq - Hkv;
-            bf16_t* dst = cache_v + (((int64_t)b * Hkv + vh) * capacity + pos) * 128;
-            const bf16_t* src = row + h * 128;
-            dst[lane] = src[lane];
-            dst[lane + 64] = src[lane + 64];
+    const uint4 c4 = *reinterpret_cast<const uint4*>(cos_t + (int64_t)pos * 128 + 8 * i);
+    const uint4 s4 = *reinterpret_cast<const uint4*>(sin_t + (int64_t)pos * 128 + 8 * i);
+    const uint4 qg = *reinterpret_cast<const uint4*>(qw + 8 * i);
+    const uint4 kg = *reinterpret_cast<const uint4*>(kw + 8 * i);
+    const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w}, sw[4] = {s4.x, s4.y, s4.z, s4.w};
+    const float sgn = i < 8 ? -1.f : 1.f;  // d < 64 takes -x[d+64] sin, d >= 64 takes +x[d-64] sin
+    const int H = Hq + 2 * Hkv;
+    for (int h0 = 4 * wave; h0 < H; h0 += 4 * (THREADS / 64)) {
+        const int h = min(h0 + grp, H - 1);  // groups past the last head redo it and store nothing
+        const uint4 x4 = *reinterpret_cast<const uint4*>(row + h * 128 + 8 * i);
+        const uint32_t xw[4] = {x4.x, x4.y, x4.z, x4.w};
+        const bool is_q = h < Hq;
+        const uint32_t gw[4] = {is_q ? qg.x : kg.x, is_q ? qg.y : kg.y, is_q ? qg.z : kg.z, is_q ? qg.w : kg.w};
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ss += bflo(xw[e]) * bflo(xw[e]);
+            ss += bfhi(xw[e]) * bfhi(xw[e]);
         }
+        const float inv = inv_rms(row16_sum(ss), 128, eps);
+        uint32_t nw[4], pw[4], ow[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            nw[e] = pack2(norm_elem(bflo(xw[e]), inv, bflo(gw[e])), norm_elem(bfhi(xw[e]), inv, bfhi(gw[e])));
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            pw[e] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)nw[e], 0x128, 0xf, 0xf, false);  // row_ror:8
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = rbf(bflo(nw[e]) * bflo(cw[e])) + rbf(sgn * bflo(pw[e]) * bflo(sw[e]));
+            const float hi = rbf(bfhi(nw[e]) * bfhi(cw[e])) + rbf(sgn * bfhi(pw[e]) * bfhi(sw[e]));
+            ow[e] = pack2(f2bf(lo), f2bf(hi));
+        }
+        if (h0 + grp >= H) continue;
+        bf16_t* dst;
+        uint4 v;
+        if (is_q) {
+            dst = q_out + ((int64_t)bt * Hq + h) * 128;
+            v = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        } else if (h < Hq + Hkv) {
+            dst = cache_k + (((int64_t)b * Hkv + (h - Hq)) * capacity + pos) * 128;
+            v = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        } else {
+            dst = cache_v + (((int64_t)b * Hkv + (h - Hq - Hkv)) * capacity + pos) * 128;
+            v = x4;
+        }
+        *reinterpret_cast<uint4*>(dst + 8 * i) = v;
     }
 }
 
