@@ -91,5 +91,6 @@ def test_noalloc_projection_rejects_oversize_before_any_launch():
     assert _lib.call("q3_skinny_ws_floats", M, N, K) > _lib.call("q3_skinny_scratch_floats")
     rc = _lib.lib().q3_skinny_tiled_noalloc(1, K, 1, M, N, K, _lib.EPI_STORE, 1, N, None)
     assert rc == 2  # hipErrorOutOfMemory
-    # The largest decode projection (qkv at 64 rows) fits.
-    assert _lib.call("q3_skinny_ws_floats", 64, 6144, 2560) <= _lib.call("q3_skinny_scratch_floats")
+    # Every decode projection at 64 rows fits (o and down, 8 splits, are the largest).
+    for N, K in ((6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)):
+        assert _lib.call("q3_skinny_ws_floats", 64, N, K) <= _lib.call("q3_skinny_scratch_floats")

@@ -37,7 +37,8 @@ def both(M, N, K, epi, seed):
 
 def test_noalloc_matches_the_workspace_entry_point():
     limit = call("q3_skinny_scratch_floats")
-    cases = [(64, 6144, 2560, _lib.EPI_STORE, 1),   # qkv at 64 rows: 5 splits, the largest decode partials
+    cases = [(64, 2560, 9728, _lib.EPI_RESID, 1),   # down at 64 rows: 8 splits, the largest decode partials
+             (64, 6144, 2560, _lib.EPI_STORE, 5),   # qkv at 64 rows: 2 splits (both on the loader-wave kernel)
              (16, 2560, 9728, _lib.EPI_RESID, 2),   # down at 16 rows: 8 splits
              (9, 2560, 4096, _lib.EPI_STORE, 3),    # o at 9 rows: 8 splits, smaller still
              (5, 19456, 2560, _lib.EPI_SWIGLU, 4)]  # gate/up: one split, no partials
