@@ -66,3 +66,28 @@ def test_gates():
         g = protocol.gates({**ok, key: bad}, native)
         assert not g["passed"], key
     assert not protocol.gates(ok, native, failing_tokens=1)["passed"]
+
+
+def test_prompt_lookup_drafts_miss_on_the_seeded_streams():
+    """Why exact-verification speculative decoding is not built: on the seeded
+    random-init workloads a prompt-lookup draft (the next k tokens after the
+    latest earlier match of the last n tokens of prompt + output) is never the
+    greedy continuation, so every verification pass would be pure cost.
+    Measured on the HF greedy streams of configs 1 and 2 (committed fixtures)."""
+    import numpy as np
+    golden = pathlib.Path(__file__).resolve().parent / "golden"
+    for name in ("config1_bf16", "config2_bf16"):
+        d = np.load(golden / f"{name}.npz")
+        ctx, out = d["ids"][0].tolist(), d["tokens"].tolist()
+        for n in (1, 2, 3):
+            accepted, i, c = 0, 0, list(ctx)
+            while i < len(out):
+                key = c[-n:]
+                draft = next((c[j + n:j + n + 4] for j in range(len(c) - n - 1, -1, -1) if c[j:j + n] == key), [])
+                a = 0
+                while a < len(draft) and i + a < len(out) and draft[a] == out[i + a]:
+                    a += 1
+                accepted += a
+                c += out[i:i + a + 1]
+                i += a + 1
+            assert accepted == 0, (name, n, accepted)
