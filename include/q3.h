@@ -84,6 +84,16 @@ int q3_gemv_partials(int M, int N, int epi);
 int q3_gemm(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
             int epi, uint16_t *y, int ldy, hipStream_t stream);
 int q3_gemm_tiles_wide(int M, int N);
+/* The same projection split along K on the 256 x 256-tile kernel, for prompts
+ * too short to fill the CUs with whole tiles (the residual projections o and
+ * down, engine.py:439,450, at 256-4095 tokens): FP32 partials
+ * ws [splits, M, N] (splits * M * N floats), summed in split order by
+ * q3_add_rmsnorm_partials.  q3_gemm_splits(M, N, K) is the split count where
+ * that applies (else 0); q3_gemm_partials takes any splits in
+ * 1..min(16, K / 64).  Same operand rules as q3_gemm; ws 16-byte aligned. */
+int q3_gemm_splits(int M, int N, int K);
+int q3_gemm_partials(const uint16_t *x, int ldx, const uint16_t *w, int M, int N, int K,
+                     float *ws, int splits, hipStream_t stream);
 
 /* act[r, j] = bf16(bf16(silu(g)) * u), (g, u) = gu[r, 2j], gu[r, 2j + 1]:
  * swiglu (fused.py:872; engine.py:464) on interleaved gate/up rows [rows, 2I].

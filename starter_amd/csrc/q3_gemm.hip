@@ -23,6 +23,12 @@
 //   across the weight tiles, so the XCD's L2 serves the operands its
 //   concurrent workgroups share.
 //
+//   With too few tiles to fill the CUs (prompts of 256-4095 tokens on the
+//   2560-wide projections), the same kernel splits K: workgroup (split,
+//   tile) sums a contiguous range of K steps and stores its FP32 partial tile
+//   to ws [splits, M, N], summed in split order by the consumer
+//   (add_rmsnorm_partials, which also applies the next RMSNorm).
+//
 // * narrow (few tiles: small prompts and decode batches above 64): 256
 //   threads, BM x BN tiles of up to 128 x 128, LDS staged through registers.
 //
@@ -71,6 +77,7 @@ constexpr int WIDE_TCH = 256 * WIDE_CPR;             // chunks per operand tile
 constexpr int WIDE_STAGE = 2 * WIDE_TCH * 16;        // 64 KB: W tile, then x tile
 constexpr int WIDE_DPT = WIDE_TCH / WIDE_THREADS;    // direct loads per operand per thread per step
 constexpr int WIDE_GROUP = 4;                        // token tiles per raster group
+constexpr int EPI_PARTIAL = -1;                      // FP32 split partials, no rounding
 
 // Position of 16-byte chunk c of 128-byte row r: c ^ ((r >> 1) & 7).  Measured
 // on gfx950: a ds_read_b128 whose 64 lanes read rows r0..r0+15 at one logical
@@ -81,7 +88,7 @@ template <int EPI>
 __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t* __restrict__ x, int ldx,
                                                                     const bf16_t* __restrict__ w, int M, int N,
                                                                     int K, bf16_t* __restrict__ y, int ldy, int tm,
-                                                                    int tn) {
+                                                                    int tn, int splits, float* __restrict__ part) {
     __shared__ __align__(1024) char lds[2 * WIDE_STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -89,11 +96,14 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
     const int g = lane >> 4, n = lane & 15;
     const int wn = wave & 3, wm = wave >> 2;  // sub-tile: weight rows 64wn.., tokens 128wm..
 
-    // Tile order: XCD-contiguous ranges, then groups of WIDE_GROUP token tiles
-    // sweeping the weight tiles.
-    const int tiles = tm * tn;
+    // Tile order: (split, tile) pairs split-major in XCD-contiguous ranges
+    // (an XCD's workgroups share a K range), then groups of WIDE_GROUP token
+    // tiles sweeping the weight tiles.
+    const int tiles = tm * tn, total = tiles * splits;
     int t = blockIdx.x;
-    if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+    if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
+    const int split = t / tiles;
+    t -= split * tiles;
     const int per_group = WIDE_GROUP * tn;
     const int grp = t / per_group, first_m = grp * WIDE_GROUP;
     const int gsz = min(WIDE_GROUP, tm - first_m);
@@ -105,8 +115,13 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
     // Rows past M or N re-read the last row: in bounds, results not stored.
     const int r0 = tid >> 3;
     const int c0 = (tid & 7) ^ wide_swz(r0);
-    const char* wbase = reinterpret_cast<const char*>(w + (int64_t)n0 * K);
-    const char* xbase = reinterpret_cast<const char*>(x + (int64_t)m0 * ldx);
+    // This split's K steps: a contiguous range, the first steps % splits
+    // splits one step longer.
+    const int steps = K / WIDE_BK;
+    const int nk = steps / splits + (split < steps % splits ? 1 : 0);
+    const int kb = (split * (steps / splits) + min(split, steps % splits)) * WIDE_BK;
+    const char* wbase = reinterpret_cast<const char*>(w + (int64_t)n0 * K + kb);
+    const char* xbase = reinterpret_cast<const char*>(x + (int64_t)m0 * ldx + kb);
     uint32_t woff[WIDE_DPT], xoff[WIDE_DPT];
 #pragma unroll
     for (int j = 0; j < WIDE_DPT; ++j) {
@@ -162,7 +177,6 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    const int nk = K / WIDE_BK;
     issue(0, 0);
     issue(1, min(1, nk - 1) * WIDE_BK);
     wait_vmcnt<2 * WIDE_DPT>();  // stage 0 landed (stage 1 may be in flight)
@@ -192,7 +206,11 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int col = n0 + wn * 64 + 16 * i + 4 * g;
-            if (col < N) store4<EPI>(y, ldy, m, col, acc[i][j]);
+            if (col >= N) continue;
+            if constexpr (EPI == EPI_PARTIAL)
+                *reinterpret_cast<f32x4_t*>(part + ((int64_t)split * M + m) * N + col) = acc[i][j];
+            else
+                store4<EPI>(y, ldy, m, col, acc[i][j]);
         }
     }
 }
@@ -329,21 +347,25 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
 }
 
 int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y, int ldy,
-                hipStream_t stream) {
+                int splits, float* part, hipStream_t stream) {
     const int tm = (M + 255) / 256, tn = (N + 255) / 256;
-    const dim3 grid(tm * tn);
+    const dim3 grid(tm * tn * splits);
     switch (epi) {
         case Q3_EPI_STORE:
             Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_STORE>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn);
+                      ldy, tm, tn, 1, nullptr);
             break;
         case Q3_EPI_RESID:
             Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_RESID>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn);
+                      ldy, tm, tn, 1, nullptr);
             break;
         case Q3_EPI_SWIGLU:
             Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_SWIGLU>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn);
+                      ldy, tm, tn, 1, nullptr);
+            break;
+        case EPI_PARTIAL:
+            Q3_LAUNCH(gemm_wide_kernel<EPI_PARTIAL>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K,
+                      nullptr, 0, tm, tn, splits, part);
             break;
         default:
             return (int)hipErrorInvalidValue;
@@ -373,9 +395,45 @@ extern "C" int q3_gemm(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, 
         return (int)hipErrorInvalidValue;
     // A token tile's rows lie within 32-bit byte offsets of its first row.
     if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
-    if (q3_gemm_tiles_wide(M, N)) return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, stream);
+    if (q3_gemm_tiles_wide(M, N)) return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, 1, nullptr, stream);
     if (M <= 16) return launch<16, 64, 1, 4>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 32) return launch<32, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 64) return launch<64, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     return launch<128, 128, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
+}
+
+// Split-K for the wide tiling where it has fewer than WIDE_MIN_TILES tiles:
+// at most WIDE_SPLIT_WGS workgroups (one per CU: each holds 128 KB of LDS),
+// or three splits from 128 tiles on, at most 16 splits (the partial
+// consumers' limit) of at least WIDE_SPLIT_STEPS K steps each; 0 where the
+// unsplit kernels apply.  Measured on MI355X (o and down of the prompt pass,
+// N = 2560, the split GEMM plus add_rmsnorm_partials against the unsplit GEMM
+// plus rmsnorm): the pick is the fastest split count at 256-3840 tokens but
+// one (512 tokens: 12 splits 34.2 us, 8 splits 32.5), and at 1024 tokens o
+// takes 41.7 against 81.3 us, down 64.3 against 175.6; at 150 tiles three
+// splits (450 workgroups) beat two and one (o: 113 / 123 / 137 us).
+constexpr int WIDE_SPLIT_WGS = 256;
+constexpr int WIDE_SPLIT_STEPS = 4;
+constexpr int WIDE_MAX_SPLITS = 16;
+
+extern "C" int q3_gemm_splits(int M, int N, int K) {
+    if (M < 256 || N < 4 || K < WIDE_BK || K % WIDE_BK || q3_gemm_tiles_wide(M, N)) return 0;
+    const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    int64_t s = tiles >= 128 ? 3 : WIDE_SPLIT_WGS / tiles;
+    s = s < WIDE_MAX_SPLITS ? s : WIDE_MAX_SPLITS;
+    const int64_t by_k = K / WIDE_BK / WIDE_SPLIT_STEPS;
+    s = s < by_k ? s : by_k;
+    return s >= 2 ? (int)s : 0;
+}
+
+extern "C" int q3_gemm_partials(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, float* ws,
+                                int splits, hipStream_t stream) {
+    if (M < 1 || N < 4 || N % 4 || K < WIDE_BK || K % WIDE_BK || ldx % 8 || ldx < K || !x || !w || !ws ||
+        splits < 1 || splits > WIDE_MAX_SPLITS || splits > K / WIDE_BK ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(ws)) & 15))
+        return (int)hipErrorInvalidValue;
+    if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
+    const int64_t grid = (int64_t)((M + 255) / 256) * ((N + 255) / 256) * splits;
+    if (grid > (1 << 30)) return (int)hipErrorInvalidValue;
+    return launch_wide(x, ldx, w, M, N, K, EPI_PARTIAL, nullptr, 0, splits, ws, stream);
 }

@@ -201,6 +201,7 @@ class Engine:
         self.graph = None
         self.keep_logits = False
         self._prefill_bufs = {}
+        self._prefill_part = None
         _log(f"loaded {self.LAYERS} layers in {time.monotonic() - self.started:.1f}s; "
              f"qkv and gate_up packed")
 
@@ -240,6 +241,7 @@ class Engine:
         self._release_graph()
         self.cache_k = self.cache_v = None
         self._prefill_bufs = {}
+        self._prefill_part = None
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
 
@@ -542,6 +544,14 @@ class Engine:
             self._prefill_bufs[rows] = bufs
         return bufs
 
+    def _prefill_partials(self, floats: int) -> torch.Tensor:
+        """FP32 split-K partials of the prompt pass's residual projections
+        (at most a few splits x 4095 rows x hidden), grown on demand."""
+        if self._prefill_part is None or self._prefill_part.numel() < floats:
+            self._prefill_part = None
+            self._prefill_part = self._empty(floats, dtype=torch.float32)
+        return self._prefill_part
+
     def _forward_prefill(self, ids: torch.Tensor, seq_len: int) -> torch.Tensor:
         """Consume the prompt ``ids [B, P]``; return the last position's logits [B, 1, V].
 
@@ -576,11 +586,18 @@ class Engine:
                 bufs = self._prefill_buffers(B * min(chunk, seq_len))
                 chunk_ids = ids[:, start:stop].contiguous()
                 resid, n, qkv, q, a, act = (_ptr(bufs[k]) for k in ("resid", "n", "qkv", "q", "a", "act"))
+                # Prompts too short to fill the CUs with whole 256 x 256 tiles split the
+                # residual projections along K; their partials are summed (in split
+                # order), joined to the residual and normalised by one row kernel,
+                # which replaces the RMSNorm that follows each of them.
+                s_o = call("q3_gemm_splits", M, H, self.q_size)
+                s_d = call("q3_gemm_splits", M, H, I)
+                part = _ptr(self._prefill_partials(max(s_o, s_d) * M * H)) if s_o or s_d else None
                 for i, L in enumerate(self.layers):
                     if i == 0:
                         call("q3_embed_rmsnorm", _ptr(chunk_ids), _ptr(self.embed), resid, n,
                              _ptr(L["in_ln"]), M, H, self.EPS, s)
-                    else:
+                    elif not s_d:  # else the previous layer's down reduction normalised it
                         call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), n, H, M, H, self.EPS, s)
                     call("q3_gemm", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
                          self.qkv_size, s)
@@ -591,11 +608,23 @@ class Engine:
                          start, Hq, Hkv, C, self.SCALE, s)
                     # Residual join and SwiGLU in the GEMM epilogues, at the reference's
                     # rounding points: resid = bf16(resid + bf16(acc)); act = bf16(bf16(silu(g)) * u).
-                    call("q3_gemm", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
-                         resid, H, s)
-                    call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), n, H, M, H, self.EPS, s)
+                    if s_o:
+                        call("q3_gemm_partials", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, part, s_o, s)
+                        call("q3_add_rmsnorm_partials", part, s_o, resid, _ptr(L["post_ln"]), n, M, H,
+                             self.EPS, s)
+                    else:
+                        call("q3_gemm", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
+                             resid, H, s)
+                        call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), n, H, M, H, self.EPS, s)
                     call("q3_gemm", n, H, _ptr(L["gate_up"]), M, 2 * I, H, _lib.EPI_SWIGLU, act, I, s)
-                    call("q3_gemm", act, I, _ptr(L["down"]), M, H, I, _lib.EPI_RESID, resid, H, s)
+                    if s_d:
+                        # The last layer's norm output is not used: the LM head
+                        # normalises the last positions of resid itself.
+                        nxt = self.layers[i + 1]["in_ln"] if i + 1 < len(self.layers) else self.final_norm
+                        call("q3_gemm_partials", act, I, _ptr(L["down"]), M, H, I, part, s_d, s)
+                        call("q3_add_rmsnorm_partials", part, s_d, resid, _ptr(nxt), n, M, H, self.EPS, s)
+                    else:
+                        call("q3_gemm", act, I, _ptr(L["down"]), M, H, I, _lib.EPI_RESID, resid, H, s)
                 last = bufs["resid"][(T - 1):]  # row T-1 of sequence 0; sequences are T rows apart
             # The final norm is applied on the last position only, then the tied LM head
             # (reference :800-803: the last layer's closing norm uses final_norm_w).

@@ -94,3 +94,23 @@ def test_noalloc_projection_rejects_oversize_before_any_launch():
     # Every decode projection at 64 rows fits (o and down, 8 splits, are the largest).
     for N, K in ((6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)):
         assert _lib.call("q3_skinny_ws_floats", 64, N, K) <= _lib.call("q3_skinny_scratch_floats")
+
+
+def test_prompt_gemm_split_policy():
+    """Split-K on the 256 x 256 tiling only below its tile threshold: about one
+    workgroup per CU, three splits from 128 tiles, at most 16 splits of >= 4
+    K steps; none for decode-sized M or where whole tiles fill the CUs."""
+    H = 2560
+    assert _lib.call("q3_gemm_splits", 1024, H, 4096) == 6
+    assert _lib.call("q3_gemm_splits", 1024, H, 9728) == 6
+    assert _lib.call("q3_gemm_splits", 256, H, 4096) == 16
+    assert _lib.call("q3_gemm_splits", 512, H, 4096) == 12
+    assert _lib.call("q3_gemm_splits", 3840, H, 4096) == 3
+    assert _lib.call("q3_gemm_splits", 3072, H, 9728) == 2
+    assert _lib.call("q3_gemm_splits", 255, H, 4096) == 0       # narrow tiles
+    assert _lib.call("q3_gemm_splits", 4096, H, 4096) == 0      # 160 whole tiles
+    assert _lib.call("q3_gemm_splits", 8192, H, 9728) == 0
+    assert _lib.call("q3_gemm_splits", 1024, H, 320) == 0       # 5 K steps: no split of >= 4 steps
+    assert _lib.call("q3_gemm_splits", 700, 3800, 576) == 2
+    with pytest.raises(RuntimeError, match="q3_gemm_partials failed"):
+        _lib.call("q3_gemm_partials", None, 4096, None, 1024, H, 4096, None, 17, None)  # > 16 splits

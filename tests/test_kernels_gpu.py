@@ -403,6 +403,52 @@ def test_gemm_wide(M, N, K, epi):
         assert_nearly_exact(out[rows, :cols], want, frac=0.06, max_ulp=2)
 
 
+@pytest.mark.parametrize("M,N,K", [(1024, 2560, 4096), (1024, 2560, 9728), (300, 2560, 4096),
+                                   (2049, 2560, 640), (700, 3800, 576)])
+def test_gemm_partials(M, N, K):
+    """Split-K partials of the 256 x 256-tile path (prompts of 256-4095 tokens):
+    at the split count q3_gemm_splits picks and at a ragged one (K steps not a
+    multiple of the splits, some splits one step long), the partials summed in
+    split order against float64 dot products on sampled rows (first, last,
+    random), nothing written past splits * M * N floats, and
+    q3_add_rmsnorm_partials on them: the residual bit-exact against the same
+    split-order FP32 sum rounded on the CPU, the norm bit-exact against
+    q3_rmsnorm of that residual and near the oracle's (an FP32 mean of squares
+    summed in another order moves a row's scale by an ulp, and the gain's
+    second rounding can double that to two BF16 ulps)."""
+    steps = K // 64
+    pick = call("q3_gemm_splits", M, N, K)
+    assert pick >= 2
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    x, w = rnd((M, K), 1.0, M + 31), rnd((N, K), 0.02, N + K + 31)
+    res = rnd((M, N), 1.0, 33)
+    gain = (1 + rnd((N,), 0.2, 34).float()).to(torch.bfloat16)
+    xd, wd, gd = dv(x), dv(w), dv(gain)
+    rows = torch.cat([torch.tensor([0, M - 1]), torch.randint(0, M, (62,), generator=g)])
+    for splits in sorted({pick, min(7, steps)}):
+        ws = dv(torch.full(((splits + 1) * M * N,), 123.0))
+        call("q3_gemm_partials", P(xd), K, P(wd), M, N, K, P(ws), splits, S())
+        torch.cuda.synchronize()
+        part = ws.cpu()
+        assert torch.all(part[splits * M * N:] == 123.0)
+        part = part[:splits * M * N].view(splits, M, N)
+        acc = part[0].clone()
+        for s_ in range(1, splits):
+            acc += part[s_]
+        check_projection(acc[rows].bfloat16(), x[rows], w)
+        rd = dv(res)
+        y = dv(torch.empty(M, N, dtype=torch.bfloat16))
+        call("q3_add_rmsnorm_partials", P(ws), splits, P(rd), P(gd), P(y), M, N, 1e-6, S())
+        torch.cuda.synchronize()
+        want = (res.float() + acc.bfloat16().float()).bfloat16()
+        assert torch.equal(rd.cpu(), want), splits
+        y_ref = dv(torch.empty(M, N, dtype=torch.bfloat16))
+        call("q3_rmsnorm", P(dv(want)), N, P(gd), P(y_ref), N, M, N, 1e-6, S())
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), y_ref.cpu())
+        assert_nearly_exact(y, oc.rms_norm(want, gain, 1e-6), max_ulp=2)
+
+
 @pytest.mark.parametrize("rows,I", [(1, 8), (7, 1024), (300, 9728), (640, 9728)])
 def test_swiglu_rows_matches_fused_epilogue(rows, I):
     """q3_swiglu_rows on a stored gate/up projection == the GEMM's fused SwiGLU

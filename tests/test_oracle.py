@@ -235,6 +235,13 @@ def test_reorder_floor_config1(full_ckpt):
           f"free-running equal through step {d - 1}", flush=True)
     assert 0.05 < max(errs) <= 0.2
     assert all(gap <= 0.4 for _, gap in flips)
+    # The first-step floor the GPU tests bound the engine by (reorder_floor.json,
+    # make_reorder_floor.py) is this same measurement.
+    import json
+
+    from conftest import GOLDEN
+    floor = json.loads((GOLDEN / "reorder_floor.json").read_text())["config1_bf16"]
+    assert abs(errs[1] - floor["first_max_abs"]) < 1e-6
     if d < n:
         hit = np.nonzero(g["top_ids"][d] == got[d])[0]
         assert g["top_logits"][d][0] - g["top_logits"][d][hit[0]] <= 0.0625

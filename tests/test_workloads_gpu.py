@@ -13,6 +13,15 @@ The bar, with its numbers measured rather than chosen:
     512-id subset), flipping the argmax at 46 of those steps at HF gaps up to
     0.156.  The north star's "max-abs <= 5e-2" is below that floor for any
     BF16 forward that sums in another order than HF's CPU path.
+  * the first step's logits over the whole vocabulary (151,936 values, an
+    extreme-value statistic of that noise): max-abs and mean-abs within
+    FLOOR_FACTOR of the same reordering's at that step
+    (tests/golden/reorder_floor.json, written by make_reorder_floor.py: 0.156
+    and 0.027-0.030 at configs 1 and 2).  Measured at config 2: the engine at
+    0.253 / 0.035 with the prompt pass's split-K residual projections, 0.213 /
+    0.037 without them -- the split sums sit closer to HF on average (a third
+    fewer logits off by more than 0.125), and one logit's excursion decides
+    the max.
   * FLOOR_FACTOR = 2: at configs 3-5 (no HF fixtures: the oracle from a
     pre-filled cache) the test measures that floor beside the engine, on the
     same cache and stream, and bounds the engine's max-abs and mean-abs by
@@ -52,6 +61,16 @@ PREFILLED_STEPS = 4
 def golden(name):
     from conftest import GOLDEN
     return np.load(GOLDEN / f"{name}.npz")
+
+
+def _reorder_floor():
+    import json
+
+    from conftest import GOLDEN
+    return json.loads((GOLDEN / "reorder_floor.json").read_text())
+
+
+REORDER_FLOOR = _reorder_floor()
 
 
 @pytest.fixture(scope="module")
@@ -106,13 +125,18 @@ def check_against_hf(eng, name, n):
     lg = logits[:, 0].float().numpy()
     sub = np.abs(lg[:, g["subset"]] - g["subset_logits"][:n]).max(axis=1)
     first = np.abs(lg[0] - g["logits_first"]).max()
+    first_mean = np.abs(lg[0] - g["logits_first"]).mean()
     last = np.abs(lg[-1] - g["logits_last"]).max() if n == len(g["tokens"]) else 0.0
     assert [s[0] for s in steps] == r["argmax"][:, 0].tolist()  # the two graphs choose alike
     print(f"{name}: free-running equal to HF through step {d - 1} of {n} (gap there {gap}); "
-          f"teacher-forced: logit max-abs first {first:.3f} last {last:.3f} subset {sub.max():.3f}, "
+          f"teacher-forced: logit max-abs first {first:.3f} (mean {first_mean:.4f}) last {last:.3f} "
+          f"subset {sub.max():.3f}, "
           f"replay top {top_err:.3f} token {tok_err:.3f}; argmax flips at {len(flips)} steps, "
           f"worst shortfall {short.max():.4f}", flush=True)
-    assert first <= TOL_FULL and last <= TOL_FULL and sub.max() <= TOL_FULL
+    floor = REORDER_FLOOR[name]
+    assert first <= FLOOR_FACTOR * floor["first_max_abs"], (first, floor)
+    assert first_mean <= FLOOR_FACTOR * floor["first_mean_abs"], (first_mean, floor)
+    assert last <= TOL_FULL and sub.max() <= TOL_FULL
     return got
 
 
