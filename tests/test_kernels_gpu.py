@@ -679,7 +679,8 @@ def test_skinny_argmax(M, N, K):
     assert pos.item() == 3 and counter.item() == 0
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 2560, 4096), (16, 2560, 9728), (64, 2560, 9728), (9, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(5, 2560, 4096), (16, 2560, 9728), (64, 2560, 9728), (64, 2560, 4096),
+                                   (40, 2560, 4096), (9, 512, 1024)])
 def test_add_rmsnorm_partials(M, N, K):
     """Partials + residual + RMSNorm in one kernel == RESID epilogue then q3_rmsnorm, bit for bit."""
     x, w = rnd((M, K), 1.0, 21), rnd((N, K), 0.02, 22)
