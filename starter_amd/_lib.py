@@ -34,6 +34,8 @@ SIGNATURES = {
     "q3_gemm_tiles_wide": [_I, _I],
     "q3_gemm_splits": [_I, _I, _I],
     "q3_gemm_partials": [_P, _I, _P, _I, _I, _I, _P, _I, _P],
+    "q3_gemm_ws_floats": [_I, _I, _I],
+    "q3_gemm_ws": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_swiglu_rows": [_P, _P, _I, _I, _P],
     "q3_skinny": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "q3_skinny_tiled": [_P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _P],
@@ -69,7 +71,7 @@ _RESTYPES = {"q3_error_string": ctypes.c_char_p}
 #: entry points that return a count, not an error code
 _COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words",
            "q3_skinny_splits", "q3_skinny_ws_floats", "q3_skinny_scratch_floats", "q3_gemm_tiles_wide",
-           "q3_gemm_splits"}
+           "q3_gemm_splits", "q3_gemm_ws_floats"}
 
 _LIB: ctypes.CDLL | None = None
 

@@ -84,11 +84,31 @@ constexpr int EPI_PARTIAL = -1;                      // FP32 split partials, no 
 // chunk (four k groups) runs at the linear-read rate; no swizzle is 2.5x slower.
 __device__ __forceinline__ int wide_swz(int r) { return (r >> 1) & 7; }
 
+// Origin of tile t of a tm x tn grid in raster order: groups of WIDE_GROUP
+// token tiles sweeping the weight tiles (the group's token tiles share each
+// weight tile while it is in L2).
+__device__ __forceinline__ void wide_origin(int t, int tm, int tn, int& m0, int& n0) {
+    const int per_group = WIDE_GROUP * tn;
+    const int grp = t / per_group, first_m = grp * WIDE_GROUP;
+    const int gsz = min(WIDE_GROUP, tm - first_m);
+    const int in_g = t - grp * per_group;
+    m0 = (first_m + in_g % gsz) * 256;
+    n0 = (in_g / gsz) * 256;
+}
+
+// Workgroups 0..full-1 take whole tiles 0..full-1 with the epilogue EPI; the
+// rest take tiles full..tm*tn-1, each split over `splits` contiguous K ranges,
+// and store FP32 partials: with EPI_PARTIAL (full == 0) to part [split, M, N],
+// else to the compact part [split, tile - full, 256, 256] that
+// wide_tail_reduce_kernel sums and finishes.  Both sets run in XCD-contiguous
+// ranges (split-major for the split tiles, so an XCD's workgroups share a K
+// range).
 template <int EPI>
 __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t* __restrict__ x, int ldx,
                                                                     const bf16_t* __restrict__ w, int M, int N,
                                                                     int K, bf16_t* __restrict__ y, int ldy, int tm,
-                                                                    int tn, int splits, float* __restrict__ part) {
+                                                                    int tn, int full, int splits,
+                                                                    float* __restrict__ part) {
     __shared__ __align__(1024) char lds[2 * WIDE_STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -96,30 +116,33 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
     const int g = lane >> 4, n = lane & 15;
     const int wn = wave & 3, wm = wave >> 2;  // sub-tile: weight rows 64wn.., tokens 128wm..
 
-    // Tile order: (split, tile) pairs split-major in XCD-contiguous ranges
-    // (an XCD's workgroups share a K range), then groups of WIDE_GROUP token
-    // tiles sweeping the weight tiles.
-    const int tiles = tm * tn, total = tiles * splits;
-    int t = blockIdx.x;
-    if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
-    const int split = t / tiles;
-    t -= split * tiles;
-    const int per_group = WIDE_GROUP * tn;
-    const int grp = t / per_group, first_m = grp * WIDE_GROUP;
-    const int gsz = min(WIDE_GROUP, tm - first_m);
-    const int in_g = t - grp * per_group;
-    const int m0 = (first_m + in_g % gsz) * 256, n0 = (in_g / gsz) * 256;
+    const int tiles = tm * tn, tail = tiles - full;
+    const int bid = blockIdx.x;
+    int t, split = 0, ns = 1;
+    if (bid < full) {
+        t = bid;
+        if ((full & 7) == 0) t = (t & 7) * (full >> 3) + (t >> 3);
+    } else {
+        const int nt = tail * splits;
+        int v = bid - full;
+        if ((nt & 7) == 0) v = (v & 7) * (nt >> 3) + (v >> 3);
+        split = v / tail;
+        t = full + (v - split * tail);
+        ns = splits;
+    }
+    int m0, n0;
+    wide_origin(t, tm, tn, m0, n0);
 
     // Direct load j of thread tid fills chunk j*512 + tid of an operand tile:
     // row 64j + tid/8, position tid%8 (wide_swz(r0 + 64j) == wide_swz(r0)).
     // Rows past M or N re-read the last row: in bounds, results not stored.
     const int r0 = tid >> 3;
     const int c0 = (tid & 7) ^ wide_swz(r0);
-    // This split's K steps: a contiguous range, the first steps % splits
-    // splits one step longer.
+    // This split's K steps: a contiguous range, the first steps % ns splits
+    // one step longer.
     const int steps = K / WIDE_BK;
-    const int nk = steps / splits + (split < steps % splits ? 1 : 0);
-    const int kb = (split * (steps / splits) + min(split, steps % splits)) * WIDE_BK;
+    const int nk = steps / ns + (split < steps % ns ? 1 : 0);
+    const int kb = (split * (steps / ns) + min(split, steps % ns)) * WIDE_BK;
     const char* wbase = reinterpret_cast<const char*>(w + (int64_t)n0 * K + kb);
     const char* xbase = reinterpret_cast<const char*>(x + (int64_t)m0 * ldx + kb);
     uint32_t woff[WIDE_DPT], xoff[WIDE_DPT];
@@ -207,12 +230,44 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
         for (int i = 0; i < 4; ++i) {
             const int col = n0 + wn * 64 + 16 * i + 4 * g;
             if (col >= N) continue;
-            if constexpr (EPI == EPI_PARTIAL)
+            if constexpr (EPI == EPI_PARTIAL) {
                 *reinterpret_cast<f32x4_t*>(part + ((int64_t)split * M + m) * N + col) = acc[i][j];
-            else
-                store4<EPI>(y, ldy, m, col, acc[i][j]);
+            } else {
+                if (ns == 1) {
+                    store4<EPI>(y, ldy, m, col, acc[i][j]);
+                } else {
+                    float* dst = part + (((int64_t)split * tail + (t - full)) * 256 + (m - m0)) * 256 + (col - n0);
+                    *reinterpret_cast<f32x4_t*>(dst) = acc[i][j];
+                }
+            }
         }
     }
+}
+
+// The split tiles of gemm_wide_kernel: partials summed in split order, then
+// the epilogue, as the unsplit tiles apply it to their own FP32 sums.  A
+// workgroup covers four rows of one tile; thread: one row, four columns.
+constexpr int TAIL_MAX_SPLITS = 8;
+
+template <int EPI>
+__global__ __launch_bounds__(256) void wide_tail_reduce_kernel(const float* __restrict__ part, int splits, int tail,
+                                                               int full, int tm, int tn, int M, int N, bf16_t* y,
+                                                               int ldy) {
+    const int ti = blockIdx.x >> 6;
+    const int r = (blockIdx.x & 63) * 4 + (threadIdx.x >> 6), c = (threadIdx.x & 63) * 4;
+    int m0, n0;
+    wide_origin(full + ti, tm, tn, m0, n0);
+    if (m0 + r >= M || n0 + c >= N) return;
+    const float* src = part + ((int64_t)ti * 256 + r) * 256 + c;
+    const int64_t stride = (int64_t)tail * 256 * 256;
+    f32x4_t p[TAIL_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < TAIL_MAX_SPLITS; ++s) p[s] = *reinterpret_cast<const f32x4_t*>(src + min(s, splits - 1) * stride);
+    f32x4_t a = p[0];
+#pragma unroll
+    for (int s = 1; s < TAIL_MAX_SPLITS; ++s)
+        if (s < splits) a += p[s];
+    store4<EPI>(y, ldy, m0 + r, n0 + c, a);
 }
 
 // ---------------------------------------------------------------- narrow
@@ -346,30 +401,42 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
     Q3_CHECK_LAUNCH();
 }
 
+// Whole tiles 0..full-1, then the rest split `splits` ways (EPI_PARTIAL:
+// full == 0, partials [splits, M, N]; other epilogues: compact partials
+// finished by wide_tail_reduce_kernel, launched here after the GEMM).
 int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y, int ldy,
-                int splits, float* part, hipStream_t stream) {
+                int full, int splits, float* part, hipStream_t stream) {
     const int tm = (M + 255) / 256, tn = (N + 255) / 256;
-    const dim3 grid(tm * tn * splits);
+    const int tail = tm * tn - full;
+    const dim3 grid(full + tail * splits);
+    const bool reduce = epi != EPI_PARTIAL && tail > 0;
+    if (reduce && (splits < 2 || splits > TAIL_MAX_SPLITS || !part)) return (int)hipErrorInvalidValue;
+#define Q3_WIDE(E)                                                                                               \
+    Q3_LAUNCH(gemm_wide_kernel<E>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y, ldy, tm, tn, full, \
+              splits, part);                                                                                     \
+    if (reduce) {                                                                                                \
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return (int)e;                                     \
+        Q3_LAUNCH(wide_tail_reduce_kernel<E>, dim3(tail * 64), dim3(256), 0, stream, part, splits, tail, full,   \
+                  tm, tn, M, N, y, ldy);                                                                         \
+    }
     switch (epi) {
         case Q3_EPI_STORE:
-            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_STORE>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn, 1, nullptr);
+            Q3_WIDE(Q3_EPI_STORE);
             break;
         case Q3_EPI_RESID:
-            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_RESID>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn, 1, nullptr);
+            Q3_WIDE(Q3_EPI_RESID);
             break;
         case Q3_EPI_SWIGLU:
-            Q3_LAUNCH(gemm_wide_kernel<Q3_EPI_SWIGLU>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y,
-                      ldy, tm, tn, 1, nullptr);
+            Q3_WIDE(Q3_EPI_SWIGLU);
             break;
         case EPI_PARTIAL:
             Q3_LAUNCH(gemm_wide_kernel<EPI_PARTIAL>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K,
-                      nullptr, 0, tm, tn, splits, part);
+                      nullptr, 0, tm, tn, 0, splits, part);
             break;
         default:
             return (int)hipErrorInvalidValue;
     }
+#undef Q3_WIDE
     Q3_CHECK_LAUNCH();
 }
 
@@ -395,11 +462,74 @@ extern "C" int q3_gemm(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, 
         return (int)hipErrorInvalidValue;
     // A token tile's rows lie within 32-bit byte offsets of its first row.
     if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
-    if (q3_gemm_tiles_wide(M, N)) return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, 1, nullptr, stream);
+    if (q3_gemm_tiles_wide(M, N))
+        return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, ((M + 255) / 256) * ((N + 255) / 256), 1, nullptr,
+                           stream);
     if (M <= 16) return launch<16, 64, 1, 4>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 32) return launch<32, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     if (M <= 64) return launch<64, 64, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
     return launch<128, 128, 2, 2>(x, ldx, w, M, N, K, epi, y, ldy, stream);
+}
+
+// Compute units of the current device (cached per device; 0 if unknown).
+static int cu_count() {
+    constexpr int MAX_DEV = 64;
+    static int cached[MAX_DEV];  // 0 = not yet asked; -1 = unknown
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        const bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+        cached[dev] = ok && cus > 0 ? cus : -1;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
+// Split tail of the wide tiling.  One 256 x 256-tile workgroup fits a CU
+// (128 KB of LDS), so the tiles run in rounds of `cus`; when the last round
+// is at most half full, its tiles are split along K over about `cus`
+// workgroups (at most TAIL_MAX_SPLITS splits of >= WIDE_SPLIT_STEPS K
+// steps), which shortens that round by the split count, and
+// wide_tail_reduce_kernel finishes them.  The partials take
+// tail * splits <= cus tiles of 256 x 256 FP32.
+struct WidePlan {
+    int full, tail, splits;
+};
+constexpr int WIDE_SPLIT_STEPS = 4;
+
+static WidePlan wide_tail_plan(int M, int N, int K) {
+    const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    const int cus = cu_count();
+    if (!q3_gemm_tiles_wide(M, N) || cus <= 0) return {tiles, 0, 1};
+    const int rem = tiles % cus;
+    if (rem == 0 || 2 * rem > cus) return {tiles, 0, 1};
+    int s = cus / rem;
+    s = s < TAIL_MAX_SPLITS ? s : TAIL_MAX_SPLITS;
+    const int by_k = K / WIDE_BK / WIDE_SPLIT_STEPS;
+    s = s < by_k ? s : by_k;
+    if (s < 2) return {tiles, 0, 1};
+    return {tiles - rem, rem, s};
+}
+
+extern "C" int q3_gemm_ws_floats(int M, int N, int K) {
+    if (M < 1 || N < 4 || K < WIDE_BK || K % WIDE_BK) return 0;
+    const WidePlan p = wide_tail_plan(M, N, K);
+    return p.tail * p.splits * 256 * 256;
+}
+
+extern "C" int q3_gemm_ws(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y,
+                          int ldy, float* ws, hipStream_t stream) {
+    const int need = q3_gemm_ws_floats(M, N, K);
+    if (need == 0 || epi == EPI_PARTIAL) return q3_gemm(x, ldx, w, M, N, K, epi, y, ldy, stream);
+    if (!ws || (reinterpret_cast<uintptr_t>(ws) & 15)) return (int)hipErrorInvalidValue;
+    // The operand checks of q3_gemm, which would take the same wide path.
+    if (N % 4 || ldx % 8 || ldx < K || ldy % 4 || !x || !w || !y ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) ||
+        (reinterpret_cast<uintptr_t>(y) & 7))
+        return (int)hipErrorInvalidValue;
+    if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
+    const WidePlan p = wide_tail_plan(M, N, K);
+    return launch_wide(x, ldx, w, M, N, K, epi, y, ldy, p.full, p.splits, ws, stream);
 }
 
 // Split-K for the wide tiling where it has fewer than WIDE_MIN_TILES tiles:
@@ -413,7 +543,6 @@ extern "C" int q3_gemm(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, 
 // takes 41.7 against 81.3 us, down 64.3 against 175.6; at 150 tiles three
 // splits (450 workgroups) beat two and one (o: 113 / 123 / 137 us).
 constexpr int WIDE_SPLIT_WGS = 256;
-constexpr int WIDE_SPLIT_STEPS = 4;
 constexpr int WIDE_MAX_SPLITS = 16;
 
 extern "C" int q3_gemm_splits(int M, int N, int K) {
@@ -435,5 +564,5 @@ extern "C" int q3_gemm_partials(const bf16_t* x, int ldx, const bf16_t* w, int M
     if ((int64_t)256 * ldx * 2 > INT32_MAX || (int64_t)256 * K * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
     const int64_t grid = (int64_t)((M + 255) / 256) * ((N + 255) / 256) * splits;
     if (grid > (1 << 30)) return (int)hipErrorInvalidValue;
-    return launch_wide(x, ldx, w, M, N, K, EPI_PARTIAL, nullptr, 0, splits, ws, stream);
+    return launch_wide(x, ldx, w, M, N, K, EPI_PARTIAL, nullptr, 0, 0, splits, ws, stream);
 }

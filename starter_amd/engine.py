@@ -545,8 +545,9 @@ class Engine:
         return bufs
 
     def _prefill_partials(self, floats: int) -> torch.Tensor:
-        """FP32 split-K partials of the prompt pass's residual projections
-        (at most a few splits x 4095 rows x hidden), grown on demand."""
+        """FP32 split-K partials of the prompt pass's projections (the residual
+        projections of 256-4095-token chunks, or the split tail tiles of
+        q3_gemm_ws: at most 126 MB), grown on demand."""
         if self._prefill_part is None or self._prefill_part.numel() < floats:
             self._prefill_part = None
             self._prefill_part = self._empty(floats, dtype=torch.float32)
@@ -592,15 +593,20 @@ class Engine:
                 # which replaces the RMSNorm that follows each of them.
                 s_o = call("q3_gemm_splits", M, H, self.q_size)
                 s_d = call("q3_gemm_splits", M, H, I)
-                part = _ptr(self._prefill_partials(max(s_o, s_d) * M * H)) if s_o or s_d else None
+                # Longer prompts whose last round of tiles is at most half full split
+                # those tiles along K (q3_gemm_ws); the same buffer holds either.
+                floats = max(s_o, s_d) * M * H
+                for n_, k_ in ((self.qkv_size, H), (2 * I, H), (H, self.q_size), (H, I)):
+                    floats = max(floats, call("q3_gemm_ws_floats", M, n_, k_))
+                part = _ptr(self._prefill_partials(floats)) if floats else None
                 for i, L in enumerate(self.layers):
                     if i == 0:
                         call("q3_embed_rmsnorm", _ptr(chunk_ids), _ptr(self.embed), resid, n,
                              _ptr(L["in_ln"]), M, H, self.EPS, s)
                     elif not s_d:  # else the previous layer's down reduction normalised it
                         call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), n, H, M, H, self.EPS, s)
-                    call("q3_gemm", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
-                         self.qkv_size, s)
+                    call("q3_gemm_ws", n, H, _ptr(L["qkv"]), M, self.qkv_size, H, _lib.EPI_STORE, qkv,
+                         self.qkv_size, part, s)
                     call("q3_qk_norm_rope_kv", qkv, self.qkv_size, _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                          _ptr(self.cos_table), _ptr(self.sin_table), None, start, q,
                          kc0 + i * layer_stride, vc0 + i * layer_stride, B, T, Hq, Hkv, D, C, self.EPS, s)
@@ -613,10 +619,10 @@ class Engine:
                         call("q3_add_rmsnorm_partials", part, s_o, resid, _ptr(L["post_ln"]), n, M, H,
                              self.EPS, s)
                     else:
-                        call("q3_gemm", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
-                             resid, H, s)
+                        call("q3_gemm_ws", a, self.q_size, _ptr(L["o"]), M, H, self.q_size, _lib.EPI_RESID,
+                             resid, H, part, s)
                         call("q3_rmsnorm", resid, H, _ptr(L["post_ln"]), n, H, M, H, self.EPS, s)
-                    call("q3_gemm", n, H, _ptr(L["gate_up"]), M, 2 * I, H, _lib.EPI_SWIGLU, act, I, s)
+                    call("q3_gemm_ws", n, H, _ptr(L["gate_up"]), M, 2 * I, H, _lib.EPI_SWIGLU, act, I, part, s)
                     if s_d:
                         # The last layer's norm output is not used: the LM head
                         # normalises the last positions of resid itself.
@@ -624,7 +630,7 @@ class Engine:
                         call("q3_gemm_partials", act, I, _ptr(L["down"]), M, H, I, part, s_d, s)
                         call("q3_add_rmsnorm_partials", part, s_d, resid, _ptr(nxt), n, M, H, self.EPS, s)
                     else:
-                        call("q3_gemm", act, I, _ptr(L["down"]), M, H, I, _lib.EPI_RESID, resid, H, s)
+                        call("q3_gemm_ws", act, I, _ptr(L["down"]), M, H, I, _lib.EPI_RESID, resid, H, part, s)
                 last = bufs["resid"][(T - 1):]  # row T-1 of sequence 0; sequences are T rows apart
             # The final norm is applied on the last position only, then the tied LM head
             # (reference :800-803: the last layer's closing norm uses final_norm_w).

@@ -449,6 +449,65 @@ def test_gemm_partials(M, N, K):
         assert_nearly_exact(y, oc.rms_norm(want, gain, 1e-6), max_ulp=2)
 
 
+def wide_origin(t, tm, tn):
+    """Tile t's (token, weight-row) origin in the 256 x 256 tiling's raster order."""
+    per_group = 4 * tn
+    grp = t // per_group
+    first_m = 4 * grp
+    gsz = min(4, tm - first_m)
+    in_g = t - grp * per_group
+    return (first_m + in_g % gsz) * 256, (in_g // gsz) * 256
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 19456, 2560), (8192, 2560, 4096), (2600, 19456, 2560),
+                                   (1000, 17008, 1024)])
+def test_gemm_ws_split_tail(M, N, K):
+    """q3_gemm_ws: the tiles of the last, at most half-full round split along K.
+    The whole tiles are q3_gemm's bits; each split tile against float64 dot
+    products on sampled rows; RESID and SWIGLU on the split tiles bit-exact
+    against the stored projection (the same split-order sums); nothing past N
+    written (ragged M and N in the last case)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tm, tn = (M + 255) // 256, (N + 255) // 256
+    tiles = tm * tn
+    rem = tiles % cus
+    assert 0 < rem and 2 * rem <= cus, "the shape must leave a split tail on this device"
+    splits = min(cus // rem, 8, K // 64 // 4)
+    assert call("q3_gemm_ws_floats", M, N, K) == rem * splits * 65536
+    full = tiles - rem
+    g = torch.Generator().manual_seed(M + N + K + 3)
+    x, w = rnd((M, K), 1.0, M + 41), rnd((N, K), 0.02, N + K + 41)
+    xd, wd = dv(x), dv(w)
+    ws = dv(torch.empty(rem * splits * 65536, dtype=torch.float32))
+    ref = dv(torch.empty(M, N, dtype=torch.bfloat16))
+    call("q3_gemm", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(ref), N, S())
+    pad = dv(torch.full((M, N + 4), 5.0, dtype=torch.bfloat16))
+    call("q3_gemm_ws", P(xd), K, P(wd), M, N, K, _lib.EPI_STORE, P(pad), N + 4, P(ws), S())
+    torch.cuda.synchronize()
+    y, want = pad.cpu(), ref.cpu()
+    assert torch.all(y[:, N:] == 5.0)
+    y = y[:, :N].contiguous()
+    split_mask = torch.zeros(M, N, dtype=torch.bool)
+    for t in range(full, tiles):
+        m0, n0 = wide_origin(t, tm, tn)
+        split_mask[m0:m0 + 256, n0:n0 + 256] = True
+        rows = torch.unique(torch.cat([torch.tensor([m0, min(m0 + 255, M - 1)]),
+                                       torch.randint(m0, min(m0 + 256, M), (6,), generator=g)]))
+        cols = slice(n0, min(n0 + 256, N))
+        check_projection(y[rows, cols], x[rows], w[cols])
+    assert torch.equal(y[~split_mask], want[~split_mask])
+    res = rnd((M, N), 1.0, 43)
+    rd = dv(res)
+    call("q3_gemm_ws", P(xd), K, P(wd), M, N, K, _lib.EPI_RESID, P(rd), N, P(ws), S())
+    act = dv(torch.empty(M, N // 2, dtype=torch.bfloat16))
+    call("q3_gemm_ws", P(xd), K, P(wd), M, N, K, _lib.EPI_SWIGLU, P(act), N // 2, P(ws), S())
+    act_ref = dv(torch.empty(M, N // 2, dtype=torch.bfloat16))
+    call("q3_swiglu_rows", P(dv(y)), P(act_ref), M, N // 2, S())
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), (res.float() + y.float()).bfloat16())
+    assert torch.equal(act.cpu(), act_ref.cpu())
+
+
 @pytest.mark.parametrize("rows,I", [(1, 8), (7, 1024), (300, 9728), (640, 9728)])
 def test_swiglu_rows_matches_fused_epilogue(rows, I):
     """q3_swiglu_rows on a stored gate/up projection == the GEMM's fused SwiGLU
