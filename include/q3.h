@@ -96,9 +96,10 @@ int q3_gemm_partials(const uint16_t *x, int ldx, const uint16_t *w, int M, int N
                      float *ws, int splits, hipStream_t stream);
 /* q3_gemm with a workspace for the split tail of the 256 x 256 tiling: where
  * the tiles' last round on the device's CUs (one tile per CU) is at most half
- * full, those tiles are split along K and a second kernel sums their FP32
- * partials in split order and applies the epilogue; the other tiles are
- * q3_gemm's, bit for bit.  ws holds q3_gemm_ws_floats(M, N, K) floats
+ * full -- or, at 256+ tokens below q3_gemm_tiles_wide, where all the tiles
+ * fill at most half the CUs -- those tiles are split along K and a second
+ * kernel sums their FP32 partials in split order and applies the epilogue;
+ * the other tiles are q3_gemm's, bit for bit.  ws holds q3_gemm_ws_floats(M, N, K) floats
  * (0: no split tail, and q3_gemm_ws is q3_gemm), 16-byte aligned.  Same
  * operand rules as q3_gemm. */
 int q3_gemm_ws_floats(int M, int N, int K);

@@ -490,8 +490,12 @@ static int cu_count() {
 // is at most half full, its tiles are split along K over about `cus`
 // workgroups (at most TAIL_MAX_SPLITS splits of >= WIDE_SPLIT_STEPS K
 // steps), which shortens that round by the split count, and
-// wide_tail_reduce_kernel finishes them.  The partials take
-// tail * splits <= cus tiles of 256 x 256 FP32.
+// wide_tail_reduce_kernel finishes them.  Below WIDE_MIN_TILES the same
+// applies to all the tiles when they fill at most half the CUs (from 256
+// tokens; measured against the 128 x 128 tiling: qkv at 512 / 768 / 1024
+// tokens 50.7 / 59.1 / 61.8 -> 37.5 / 42.4 / 52.8 us, gate/up at 256 tokens
+// 61.8 -> 48.5).  The partials take tail * splits <= cus tiles of 256 x 256
+// FP32.
 struct WidePlan {
     int full, tail, splits;
 };
@@ -500,7 +504,7 @@ constexpr int WIDE_SPLIT_STEPS = 4;
 static WidePlan wide_tail_plan(int M, int N, int K) {
     const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
     const int cus = cu_count();
-    if (!q3_gemm_tiles_wide(M, N) || cus <= 0) return {tiles, 0, 1};
+    if (M < 256 || cus <= 0 || (!q3_gemm_tiles_wide(M, N) && 2 * tiles > cus)) return {tiles, 0, 1};
     const int rem = tiles % cus;
     if (rem == 0 || 2 * rem > cus) return {tiles, 0, 1};
     int s = cus / rem;

@@ -460,9 +460,10 @@ def wide_origin(t, tm, tn):
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 19456, 2560), (8192, 2560, 4096), (2600, 19456, 2560),
-                                   (1000, 17008, 1024)])
+                                   (1000, 17008, 1024), (1024, 6144, 2560), (256, 19456, 2560)])
 def test_gemm_ws_split_tail(M, N, K):
-    """q3_gemm_ws: the tiles of the last, at most half-full round split along K.
+    """q3_gemm_ws: the tiles of the last, at most half-full round split along K
+    (the last two shapes: every tile, below the 256 x 256 threshold).
     The whole tiles are q3_gemm's bits; each split tile against float64 dot
     products on sampled rows; RESID and SWIGLU on the split tiles bit-exact
     against the stored projection (the same split-order sums); nothing past N
