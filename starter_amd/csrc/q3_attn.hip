@@ -554,9 +554,10 @@ constexpr int PBLK = 64;                   // keys per prefill block
 constexpr int PTILE = PBLK * D * 2;        // bytes of one K (or V) block tile
 constexpr int PSTAGE = 2 * PTILE;          // K tile then V tile
 constexpr int PDMA = PBLK * 16 / THREADS;  // direct loads per tile per thread (4)
+constexpr long PREFILL_WIDE_WGS = 512;     // 32-query workgroups from this many on
 
-// grid (ceil(T/32), Hkv, B); wave w = query head kvh*4 + w, 32 queries per
-// workgroup (two MFMA column blocks of 16).  Keys advance 64 at a time through
+// grid (ceil(T/(16 CB)), Hkv, B); wave w = query head kvh*4 + w, 16 CB
+// queries per workgroup (CB MFMA column blocks of 16).  Keys advance 64 at a time through
 // two LDS stages (K and V tiles in the decode layout, kv_slot) filled by
 // direct global-to-LDS loads, so the four heads share each K/V byte and the
 // next block streams in while this one computes.  Per block and column block:
@@ -566,21 +567,22 @@ constexpr int PDMA = PBLK * 16 / THREADS;  // direct loads per tile per thread (
 // O^T += V^T.P^T (16 MFMAs, V^T through transposing LDS reads).  Workgroups
 // start with the last queries (the longest causal ranges), so the short ones
 // fill the tail of the launch.
+template <int CB>
 __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* q, const bf16_t* cache_k,
                                                                const bf16_t* cache_v, bf16_t* out,
                                                                int T, int start, int Hq, int Hkv,
                                                                int capacity, float scale) {
     __shared__ __align__(1024) char lds[2 * PSTAGE];
-    const int qb0 = (gridDim.x - 1 - blockIdx.x) * 32, kvh = blockIdx.y, b = blockIdx.z;
+    const int qb0 = (gridDim.x - 1 - blockIdx.x) * 16 * CB, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int h = kvh * GROUP + w;
 
-    // Q^T operands for the two 16-query column blocks.
-    bf16x8_t qb[2][4];
+    // Q^T operands for the 16-query column blocks.
+    bf16x8_t qb[CB][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < CB; ++cb) {
         const int qi = qb0 + 16 * cb + n;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -596,7 +598,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     // waiting for the next block's loads as well.
     q3dma::wait_vmcnt<0>();
 
-    const int q_last = min(qb0 + 31, T - 1);
+    const int q_last = min(qb0 + 16 * CB - 1, T - 1);
     const int key_end = start + q_last + 1;  // keys 0 .. start+q_last
     const int nblk = (key_end + PBLK - 1) / PBLK;
     const int full_end = start + qb0 + 1;    // keys below it are visible to every query here
@@ -621,12 +623,15 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     };
 
     const float c = scale * 1.4426950408889634f;  // scores in base-2 units
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-    f32x4_t acc[2][8];
+    float m[CB], l[CB];
+    f32x4_t acc[CB][8];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int cb = 0; cb < CB; ++cb) {
+        m[cb] = -INFINITY;
+        l[cb] = 0.f;
 #pragma unroll
         for (int dm = 0; dm < 8; ++dm) acc[cb][dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     // One 64-key block from LDS stage st: S^T, online softmax, O^T += V^T.P^T.
     // MASK: some key of the block lies past some query (blocks that cross the
@@ -635,11 +640,12 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
         constexpr bool MASK = decltype(mask_tag)::value;
         const bf16_t* kt = reinterpret_cast<const bf16_t*>(lds + st * PSTAGE);
         const bf16_t* vt = kt + PTILE / 2;
-        f32x4_t s[2][4];
+        f32x4_t s[CB][4];
 #pragma unroll
         for (int hb = 0; hb < 4; ++hb) {
             const int key = 16 * hb + n;
-            s[0][hb] = s[1][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) s[cb][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 // k slot (g, t) is d = 32kk + 8g + t on both operands: each lane group
@@ -647,13 +653,14 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
                 // linear rate (d = 32g + 8kk + t measured 30% slower).
                 const bf16x8_t kf = __builtin_bit_cast(
                     bf16x8_t, reinterpret_cast<const u32x4_t*>(kt)[kv_slot(key, 4 * kk + g)]);
-                s[0][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[0][kk], s[0][hb], 0, 0, 0);
-                s[1][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[1][kk], s[1][hb], 0, 0, 0);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+                    s[cb][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[cb][kk], s[cb][hb], 0, 0, 0);
             }
         }
-        bf16x8_t pb[2][2];
+        bf16x8_t pb[CB][2];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < CB; ++cb) {
             float mx = -INFINITY;
             if constexpr (MASK) {
                 const int qpos = start + qb0 + 16 * cb + n;  // this lane's query position
@@ -708,7 +715,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
             for (int dm = 0; dm < 8; ++dm) {
                 const bf16x8_t va = vt_operand_tr(vt + j * 32 * D, dm, lane);
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
+                for (int cb = 0; cb < CB; ++cb)
                     acc[cb][dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][j], acc[cb][dm], 0, 0, 0);
             }
     };
@@ -729,7 +736,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     q3dma::wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < CB; ++cb) {
         const int qi = qb0 + 16 * cb + n;
         if (qi < T) {
             const float inv_l = 1.0f / l[cb];
@@ -884,7 +891,16 @@ extern "C" int q3_attn_prefill(const bf16_t* q, const bf16_t* cache_k, const bf1
     if (B < 1 || T < 1 || start < 0 || Hq != GROUP * Hkv || start + T > capacity) return (int)hipErrorInvalidValue;
     // One (sequence, KV head) cache row block lies within 32-bit byte offsets.
     if ((int64_t)capacity * D * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
-    Q3_LAUNCH(attn_prefill_kernel, dim3((T + 31) / 32, Hkv, B), dim3(THREADS), 0, stream,
-                       q, cache_k, cache_v, out, T, start, Hq, Hkv, capacity, scale);
+    // 32 queries per workgroup (each K/V block serves two column blocks), or
+    // 16 where that grid would not give every CU two workgroups: the longest
+    // causal range sets the launch's length, and half the queries per block
+    // halve that workgroup's work.
+    const long wgs32 = (long)((T + 31) / 32) * Hkv * B;
+    if (wgs32 < PREFILL_WIDE_WGS)
+        Q3_LAUNCH(attn_prefill_kernel<1>, dim3((T + 15) / 16, Hkv, B), dim3(THREADS), 0, stream,
+                  q, cache_k, cache_v, out, T, start, Hq, Hkv, capacity, scale);
+    else
+        Q3_LAUNCH(attn_prefill_kernel<2>, dim3((T + 31) / 32, Hkv, B), dim3(THREADS), 0, stream,
+                  q, cache_k, cache_v, out, T, start, Hq, Hkv, capacity, scale);
     Q3_CHECK_LAUNCH();
 }
