@@ -145,6 +145,35 @@ def test_fused_mfma_decode_matches_oracle(tile_engine, tile_ckpt, batch):
     assert list(tile_engine.generate(ids, 6)) == steps
 
 
+@pytest.mark.parametrize("batch,prompt,chunk", [(4, 300, 0), (3, 700, 512)])
+def test_long_prompt_split_projections_match_oracle(tile_engine, tile_ckpt, batch, prompt, chunk):
+    """Prompt passes of 1200 rows, and of 2100 rows in chunks of 170 tokens per
+    sequence (510 rows) with a last chunk of 20 (unsplit), put the projections
+    on their split paths: o and down as split-K partials summed by add_rmsnorm_partials
+    (which also applies the next norm), qkv and gate/up split along K and
+    finished by the tail reduction (q3_gemm_ws).  First logits and the stream
+    against the CPU oracle."""
+    cfg, tensors = load_checkpoint(tile_ckpt)
+    H, I, Q = cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads * cfg.head_dim
+    QKV = Q + 2 * cfg.num_key_value_heads * cfg.head_dim
+    M = batch * (min(prompt, chunk // batch) if chunk else prompt)
+    from starter_amd._lib import call
+    assert call("q3_gemm_splits", M, H, Q) > 1 and call("q3_gemm_splits", M, H, I) > 1
+    assert call("q3_gemm_ws_floats", M, QKV, H) > 0 and call("q3_gemm_ws_floats", M, 2 * I, H) > 0
+    orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
+    rng = np.random.Generator(np.random.PCG64(200 + batch))
+    ids = rng.integers(0, cfg.vocab_size, (batch, prompt)).tolist()
+    want, want_logits = orc.generate(ids, 4, keep_logits=True)
+    saved = engine_mod.PREFILL_CHUNK_TOKENS
+    if chunk:
+        engine_mod.PREFILL_CHUNK_TOKENS = chunk
+    try:
+        steps, logits = tile_engine.trace_logits(ids, 4)
+    finally:
+        engine_mod.PREFILL_CHUNK_TOKENS = saved
+    check_stream(steps, logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
+
+
 def _trace_attention(engine, ids, n, fused):
     saved = engine_mod.FUSED_ATTENTION
     engine_mod.FUSED_ATTENTION = fused
