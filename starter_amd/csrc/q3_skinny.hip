@@ -644,13 +644,11 @@ struct Plan {
 //   qkv     N=6144  K=2560: 4 x 5 (480 workgroups) up to 32 rows; 3 x 2 (256)
 //                           above, where five splits' partials cost more than
 //                           they spread;
-//   o       N=2560  K=4096: 5 x 8 at <= 16 rows, 4 x 6 at <= 32, 4 x 4 above:
-//                           timed with the reduction that sums its partials
-//                           (add_rmsnorm_partials, one workgroup per row,
-//                           bound by the ~27 GB/s a CU streams), 4 x 4 takes
-//                           12.2 us at 64 rows against 13.7 for 5 x 8 (the
-//                           projection alone is 0.3 us slower, the reduction
-//                           1.8 us faster); at 8-16 rows they tie;
+//   o       N=2560  K=4096: 5 x 8 at <= 16 rows, 4 x 6 at <= 32, 4 x 4 above
+//                           (with the reduction of its partials, 4 x 4 and
+//                           5 x 8 take 14.3 and 14.2 us per layer in the
+//                           engine's profile at 64 rows, and the config-4 step
+//                           5.62-5.64 against 5.64-5.66 ms);
 //   gate/up N=19456 K=2560: 5 x 1 (244 workgroups, SwiGLU in the epilogue,
 //                           no partials): 22-24% faster than 4 x 2 + reduce;
 //   down    N=2560  K=9728: 5 x 8.
