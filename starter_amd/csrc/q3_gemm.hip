@@ -11,11 +11,17 @@
 // * wide (the prompt pass): a 512-thread workgroup owns a 256 x 256 output
 //   tile; eight waves, two per SIMD, each a 128 (token) x 64 (weight row)
 //   sub-tile whose 32 FP32 accumulator blocks stay in registers.  K advances
-//   64 at a time through two 64 KB LDS stages filled by global_load_lds_dwordx4
-//   (global memory straight into LDS, no register round trip).  Within a step
-//   the MFMAs of one 32-wide k half run while the fragments of the next half
-//   load (one LDS read per two MFMAs); a single barrier per step separates
-//   "stage kt+1 has landed" from "stage kt may be refilled".  Each 128-byte
+//   64 at a time through LDS filled by global_load_lds_dwordx4 (global memory
+//   straight into LDS, no register round trip): the x tiles (32 KB) in three
+//   stages, two steps ahead, and the W tiles in two, one step ahead -- the 160
+//   KB a workgroup may hold (measured on MI355X with cold weights, rotating
+//   over four copies, against two 64 KB stages of both: one 131,072-token
+//   layer's projections 21.72 -> 21.32 ms, o 2370 -> 2287 us, qkv 3369 ->
+//   3263, gate/up 10948 -> 10800, down 5033 -> 4973; three W stages instead
+//   tie at 21.29 ms).  Within a step the MFMAs of one 32-wide k half run while the
+//   fragments of the next half load (one LDS read per two MFMAs); a single
+//   barrier per step separates "step kt+1 has landed" from "step kt's stages
+//   may be refilled".  Each 128-byte
 //   tile row is one contiguous 128-byte global read (eight lanes), and its
 //   16-byte chunks are XOR-swizzled so the operand reads (16 rows, one chunk)
 //   are free of LDS bank conflicts.  Workgroup w runs on XCD w % 8; each XCD
@@ -74,7 +80,6 @@ constexpr int WIDE_THREADS = 512;
 constexpr int WIDE_BK = 64;
 constexpr int WIDE_CPR = 8;                          // 16-byte chunks per 128-byte tile row
 constexpr int WIDE_TCH = 256 * WIDE_CPR;             // chunks per operand tile
-constexpr int WIDE_STAGE = 2 * WIDE_TCH * 16;        // 64 KB: W tile, then x tile
 constexpr int WIDE_DPT = WIDE_TCH / WIDE_THREADS;    // direct loads per operand per thread per step
 constexpr int WIDE_GROUP = 4;                        // token tiles per raster group
 constexpr int EPI_PARTIAL = -1;                      // FP32 split partials, no rounding
@@ -109,7 +114,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
                                                                     int K, bf16_t* __restrict__ y, int ldy, int tm,
                                                                     int tn, int full, int splits,
                                                                     float* __restrict__ part) {
-    __shared__ __align__(1024) char lds[2 * WIDE_STAGE];
+    constexpr int WT = WIDE_TCH * 16;             // 32 KB: one operand tile
+    __shared__ __align__(1024) char lds[5 * WT];  // x tiles in three stages, then W tiles in two
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -152,14 +158,17 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
         xoff[j] = (uint32_t)((min(m0 + r0 + 64 * j, M - 1) - m0) * ldx + 8 * c0) * 2u;
     }
     const uint32_t lds_wave = lds_address(lds) + wave * 64 * 16;
-    auto issue = [&](int stage, int k0) {
-        const uint32_t base = lds_wave + stage * WIDE_STAGE;
-        const char* wb = wbase + 2 * k0;
+    auto issue_x = [&](int stage, int k0) {
+        const uint32_t base = lds_wave + stage * WT;
         const char* xb = xbase + 2 * k0;
 #pragma unroll
-        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(wb, woff[j], base + j * WIDE_THREADS * 16);
+        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(xb, xoff[j], base + j * WIDE_THREADS * 16);
+    };
+    auto issue_w = [&](int stage, int k0) {
+        const uint32_t base = lds_wave + 3 * WT + stage * WT;
+        const char* wb = wbase + 2 * k0;
 #pragma unroll
-        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(xb, xoff[j], base + WIDE_TCH * 16 + j * WIDE_THREADS * 16);
+        for (int j = 0; j < WIDE_DPT; ++j) load_to_lds(wb, woff[j], base + j * WIDE_THREADS * 16);
     };
 
     f32x4_t acc[4][8];
@@ -175,14 +184,15 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
         aoff[kk] = (ra * WIDE_CPR + ((4 * kk + g) ^ wide_swz(ra))) * 16;
-        boff[kk] = WIDE_TCH * 16 + (rb * WIDE_CPR + ((4 * kk + g) ^ wide_swz(rb))) * 16;
+        boff[kk] = (rb * WIDE_CPR + ((4 * kk + g) ^ wide_swz(rb))) * 16;
     }
-    auto load_frags = [&](int stage, int kk, u32x4_t (&a)[4], u32x4_t (&b)[8]) {
-        const char* st = lds + stage * WIDE_STAGE;
+    auto load_frags = [&](int wst, int xst, int kk, u32x4_t (&a)[4], u32x4_t (&b)[8]) {
+        const char* wp = lds + 3 * WT + wst * WT;
+        const char* xp = lds + xst * WT;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(st + aoff[kk] + i * 16 * 128);
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(wp + aoff[kk] + i * 16 * 128);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(st + boff[kk] + j * 16 * 128);
+        for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(xp + boff[kk] + j * 16 * 128);
     };
     auto mfmas = [&](const u32x4_t (&a)[4], const u32x4_t (&b)[8]) {
 #pragma unroll
@@ -200,24 +210,34 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    issue(0, 0);
-    issue(1, min(1, nk - 1) * WIDE_BK);
-    wait_vmcnt<2 * WIDE_DPT>();  // stage 0 landed (stage 1 may be in flight)
+    // x runs two K steps ahead (three stages), W one (two stages): the
+    // direct loads go out in the order x(0) W(0) x(1) W(1) x(2), then per
+    // step W(kt+2) x(kt+3), so the loads still allowed in flight when step
+    // kt+1 must have landed are exactly x(kt+2)'s.  Past the end the last K
+    // slice is loaded again (in bounds, never used), which keeps every wait
+    // count fixed.
+    issue_x(0, 0);
+    issue_w(0, 0);
+    issue_x(1, min(1, nk - 1) * WIDE_BK);
+    issue_w(1, min(1, nk - 1) * WIDE_BK);
+    issue_x(2, min(2, nk - 1) * WIDE_BK);
+    wait_vmcnt<3 * WIDE_DPT>();  // step 0 landed (x(1), W(1), x(2) may be in flight)
     __syncthreads();
     u32x4_t a0[4], b0[8], a1[4], b1[8];
-    load_frags(0, 0, a0, b0);
+    load_frags(0, 0, 0, a0, b0);
+    int xs = 0;  // x stage of step kt (kt % 3)
     for (int kt = 0; kt < nk; ++kt) {
-        const int st = kt & 1;
-        load_frags(st, 1, a1, b1);
+        const int wst = kt & 1, xn = xs == 2 ? 0 : xs + 1;
+        load_frags(wst, xs, 1, a1, b1);
         mfmas(a0, b0);
-        wait_vmcnt<0>();  // step kt+1 landed: the only direct loads in flight
+        wait_vmcnt<WIDE_DPT>();  // step kt+1 landed; x(kt+2) may be in flight
         __syncthreads();
-        // Stage kt is read no more: refill it with step kt+2.  Past the end the
-        // last K slice is loaded again (in bounds, never used), which keeps
-        // every wait count above fixed.
-        issue(st, min(kt + 2, nk - 1) * WIDE_BK);
-        load_frags(st ^ 1, 0, a0, b0);
+        // Step kt's stages are read no more: W(kt+2) and x(kt+3) refill them.
+        issue_w(wst, min(kt + 2, nk - 1) * WIDE_BK);
+        issue_x(xs, min(kt + 3, nk - 1) * WIDE_BK);
+        load_frags(wst ^ 1, xn, 0, a0, b0);
         mfmas(a1, b1);
+        xs = xn;
     }
     wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
