@@ -652,6 +652,8 @@ struct Plan {
 //   gate/up N=19456 K=2560: 5 x 1 (244 workgroups, SwiGLU in the epilogue,
 //                           no partials): 22-24% faster than 4 x 2 + reduce;
 //   down    N=2560  K=9728: 5 x 8.
+// Fewer splits at 16 rows, for a cheaper reduction (o 5 x 4, down 5 x 5),
+// measured slower in the engine: config 3 2.48 -> 2.52 ms per step.
 // Other shapes take four waves and the generic split count.
 Plan skinny_plan(int M, int N, int K) {
     const int mt = (M + 15) / 16;
