@@ -1,5 +1,5 @@
-// MFMA building blocks of decode attention shared by the split-K decode kernel
-// (q3_attn.hip) and the one-kernel decode step (q3_persist.hip).
+// MFMA building blocks of decode attention (q3_attn.hip): the per-block
+// scores, online softmax and P.V of the split-K decode kernel.
 //
 // Head_dim 128, 4 query heads per KV head, 32-key blocks.  MFMA layout
 // (v_mfma_f32_16x16x32_bf16, lane l, g = l/16, n = l%16): A[m=n][k=8g+t],
