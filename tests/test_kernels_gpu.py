@@ -824,6 +824,30 @@ def test_attn_decode_fused(B, C, pos, splits, qsplits):
     assert err.item() == 0
 
 
+def test_attn_decode_fused_rejects_layers_past_its_flag():
+    """The exchange flag holds (position, layer) with layer < 64: the launcher
+    refuses layer 64 and a negative layer before anything is enqueued, and the
+    engine keeps two launches for deeper models."""
+    Hq, Hkv, D, B, C, splits = 32, 8, 128, 1, 1536, 12
+    assert call("q3_attn_fused_grid", B, Hq, Hkv, C, splits) > 0
+    qkv = torch.zeros(B, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device=DEV)
+    gain = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    cos, sin = oc.rope_tables(5e6, D, C + 1)
+    cos, sin = dv(cos), dv(sin)
+    posd = dv(torch.tensor([5]))
+    ck = torch.zeros(B, Hkv, C, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.full((B, Hq * D), 7.0, dtype=torch.bfloat16, device=DEV)
+    for layer in (64, -1):
+        with pytest.raises(RuntimeError):
+            call("q3_attn_decode_fused", P(qkv), qkv.shape[1], None, 0, P(gain), P(gain), P(cos), P(sin), P(posd),
+                 P(ck), P(cv), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5, P(err), S())
+    torch.cuda.synchronize()
+    assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and err.item() == 0
+
+
 @pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6),
                                               # configs 5 and 4: qkv from the skinny projection's partials
                                               (8, 16512, 16500, 5), (64, 2176, 2100, 5)])
