@@ -573,7 +573,14 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
                                                                int T, int start, int Hq, int Hkv,
                                                                int capacity, float scale) {
     __shared__ __align__(1024) char lds[2 * PSTAGE];
-    const int qb0 = (gridDim.x - 1 - blockIdx.x) * 16 * CB, kvh = blockIdx.y, b = blockIdx.z;
+    // Workgroup i runs on XCD i % 8.  Taken in XCD-contiguous ranges, every
+    // query block of one (sequence, KV head) runs on one XCD, whose L2 then
+    // fetches that K/V range once instead of each XCD fetching all of it.
+    const int qbs = gridDim.x, nb = qbs * gridDim.y * gridDim.z;
+    int id = blockIdx.x + qbs * (blockIdx.y + gridDim.y * blockIdx.z);
+    if ((nb & 7) == 0) id = (id & 7) * (nb >> 3) + (id >> 3);
+    const int pair = id / qbs;
+    const int qb0 = (qbs - 1 - (id - pair * qbs)) * 16 * CB, kvh = pair % gridDim.y, b = pair / gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
