@@ -778,14 +778,19 @@ extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     // measured long contexts stream fastest at three (B=8, 16K keys: 90.2 us
     // at 12 splits against 94.4 at 8; B=16, 8K keys: 92.4 at 6 against 95.3
     // at 4), with at least 256 keys (two blocks per wave) per split; when even
-    // that leaves CUs idle (short contexts at small batch), 128 keys per split
-    // to spread the latency-bound work.
+    // that leaves CUs idle (short contexts at small batch), 96 keys per split
+    // where that is at most 16 splits (the fused merge's width), else 128, to
+    // spread the latency-bound work (B=1 at 1536 keys: a 1.836 ms step at 16
+    // splits of 96 keys, against 1.848 at 12 of 128 and 1.865 at 8 of 192).
     const long heads = (long)B * Hkv;
     if (heads >= 512 || (heads >= 128 && capacity <= 4096)) return 1;
     const long groups = heads >= 64 ? 768 : 512;
     const long want = (groups + heads - 1) / heads;
     long most = (capacity + 255) / 256;
-    if (heads * most < 128) most = (capacity + 127) / 128;
+    if (heads * most < 128) {
+        const long fine = (capacity + 95) / 96;
+        most = fine <= 16 ? fine : (capacity + 127) / 128;
+    }
     const long s = want < most ? want : most;
     return s < 1 ? 1 : (int)s;
 }

@@ -68,7 +68,9 @@ def test_attention_splits_policy():
     # One split from 128 (sequence, KV head) pairs at moderate context or 512 at any;
     # else about 512 workgroups (768 from 64 pairs) of >= 256 keys, 128-key splits while CUs would idle.
     assert _lib.call("q3_attn_splits", 1, 8, 64) == 1
-    assert _lib.call("q3_attn_splits", 1, 8, 1536) == 12
+    assert _lib.call("q3_attn_splits", 1, 8, 1536) == 16   # 96 keys per split
+    assert _lib.call("q3_attn_splits", 1, 8, 2048) == 16   # 128 (96 would take 22)
+    assert _lib.call("q3_attn_splits", 1, 8, 3000) == 24
     assert _lib.call("q3_attn_splits", 16, 8, 768) == 1
     assert _lib.call("q3_attn_splits", 16, 8, 16384) == 6
     assert _lib.call("q3_attn_splits", 64, 8, 2176) == 1
