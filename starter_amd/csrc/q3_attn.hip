@@ -772,8 +772,8 @@ extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     // enough (sequence, KV head) pairs to occupy half the CUs at moderate
     // context, or every CU twice at any context (B=64 at 2176 keys: 86.6 us
     // against 96-111 us for 3-8 splits with their merge; B=16 at 768 keys: a
-    // 2.474 ms step against 2.590 at 2 splits with the merge in the same
-    // launch and 2.628-2.646 at 3-4 with a merge launch).  Otherwise about 512
+    // 2.474 ms step against 2.590-2.646 at 2-4 splits with a merge launch,
+    // their grids being too large for the fused merge).  Otherwise about 512
     // workgroups (two resident per CU), or 768 (three) from 64 pairs on, where
     // measured long contexts stream fastest at three (B=8, 16K keys: 90.2 us
     // at 12 splits against 94.4 at 8; B=16, 8K keys: 92.4 at 6 against 95.3
