@@ -599,13 +599,15 @@ def test_attn_decode(B, C, pos, splits):
 
 
 @pytest.mark.parametrize("B,T,start", [(1, 1, 0), (2, 37, 0), (1, 64, 0), (2, 20, 30), (3, 50, 13), (1, 300, 0),
-                                       (2, 130, 70), (1, 1000, 24), (1, 97, 4000), (16, 256, 0), (4, 600, 9)])
+                                       (2, 130, 70), (1, 1000, 24), (1, 97, 4000), (16, 256, 0), (4, 600, 9),
+                                       (16, 600, 0), (8, 1024, 512)])
 def test_attn_prefill(B, T, start):
     """Chunks at offset `start` over a cache of start + T + 5 slots: one and many
     64-key blocks, blocks crossing the diagonal of some but not all queries, a
     ragged last query block, and a long prefix with a short chunk.  Grids of
-    fewer than 512 32-query workgroups take 16-query workgroups; the last two
-    shapes take 32."""
+    fewer than 512 32-query workgroups take 16-query workgroups; the last four
+    shapes take 32 (the last two in grids of 2048 or more, over several XCD
+    ranges)."""
     Hq, Hkv, D = 32, 8, 128
     C = start + T + 5
     q = rnd((B * T, Hq, D), 1.0, T)
