@@ -1,13 +1,16 @@
 """Decode throughput of the MI355X Qwen3-4B engine on one GPU.
 
-    python bench.py [--steps K] [--warmup W] [--config 2] [--extra-configs 3,4] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--config 2] [--extra-configs 1,3,4,5] [--gpus 1]
 
 A step is one decode step of the whole batch (one token per sequence): one
 replay of the captured hipGraph.  The headline workload is BASELINE config 2
 (seeded Qwen3-4B BF16, batch 1, prompt 1024, 512 new tokens): the prompt is
 prefilled (untimed), W steps warm up, then exactly K steps are timed with HIP
 events on the engine's stream, bracketed by device synchronisation.  Inputs
-(weights, KV cache, token buffers) are resident in HBM throughout.
+(weights, KV cache, token buffers) are resident in HBM throughout.  The timed
+steps are decode steps W .. W+K-1 of the workload (contexts P+W+1 ..
+P+W+K), and the step's bytes are counted at those contexts; a workload with
+fewer than W+K decode steps clamps K.
 
 Printed: one JSON line with decode tokens/s (value), ms/step, the whole-step
 HBM roofline fraction (weights + KV bytes per step over 8 TB/s), the dominant
@@ -15,11 +18,12 @@ kernel's roofline (timed live, HIP events on the engine's stream, over a
 graph of its 36 layer launches at the workload's shapes), and the CPU
 baseline: the reference engine's eager CPU decode step
 (oracle/ref_cpu_path.py) timed on this host's cores on a bounded sample of the
-workload.  Beside them, ``prefill``: the prompt's forward (warm, second call)
-timed with HIP events, as tokens/s and as a fraction of dense BF16 MFMA peak;
-and ``workloads``: the same figures for the batch-16 and batch-64 configs
-(BASELINE configs 3 and 4), each timed over all of its decode steps after the
-warm-up.
+workload (at least 8 decode steps at the workload's real cache shape; every
+decode step of config 1).  Beside them, ``prefill``: the prompt's forward
+(warm, second call) timed with HIP events, as tokens/s and as a fraction of
+dense BF16 MFMA peak; and ``workloads``: the same figures for the other
+BASELINE configs (1, 3, 4 and 5 by default), each timed over the same
+decode steps W .. W+K-1 of its own run.
 """
 
 from __future__ import annotations
@@ -115,6 +119,8 @@ def kernel_rooflines(eng, wl) -> list[dict]:
 
     B, H, I = eng.batch, eng.HIDDEN, eng.INTER
     s = eng.stream.cuda_stream
+    # Counter summaries: the projections' launches depend only on the batch
+    # (same weights and shapes at every config), attention's on the context too.
     tag = f"config{wl.number}_b{B}"
     out = []
     gate_up = 2 * I * H * 2 + B * H * 2 + B * I * 2
@@ -124,13 +130,13 @@ def kernel_rooflines(eng, wl) -> list[dict]:
             L["gate_up"].data_ptr(), B, 2 * I, H, _lib.EPI_SWIGLU, eng.act.data_ptr(), I, None, None, None, None,
             None, 0, s))
         out.append(kernel_line("gemv_dot2 gate_up (norm prologue, SwiGLU epilogue)", gate_up + H * 2, ms,
-                               f"gemv_gate_up_{tag}_traffic.txt"))
+                               f"gemv_gate_up_b{B}_traffic.txt"))
     elif eng.skinny:
         T = lambda w: eng.tiled[id(w)].data_ptr()  # noqa: E731
         ms = time_layer_graph(eng, lambda i, L: call(
             "q3_skinny_tiled", eng.nbuf.data_ptr(), H, T(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU,
             eng.act.data_ptr(), I, eng.skinny_ws.data_ptr(), s))
-        line = kernel_line("skinny MFMA gate_up (SwiGLU epilogue)", gate_up, ms, f"skinny_gate_up_{tag}_traffic.txt")
+        line = kernel_line("skinny MFMA gate_up (SwiGLU epilogue)", gate_up, ms, f"skinny_gate_up_b{B}_traffic.txt")
         line["mfma_tflops"] = round(2.0 * B * 2 * I * H / (ms * 1e-3) / 1e12, 1)
         out.append(line)
         ctx = int(eng.g_pos.item()) + 1
@@ -170,38 +176,41 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(ref, wl, budget_s: float) -> dict:
+def cpu_baseline(ref, wl, budget_s: float, min_steps: int = 8) -> dict:
     """The reference engine's eager CPU decode step (``ref``, an
     oracle.ref_cpu_path.RefCpuDecode) at this workload's cache shape: one warm
-    step, then steps until ``budget_s`` is spent (at least one).  The cache's
-    prompt positions are zero except the first few: a decode step's cost does
-    not depend on the cache's values."""
+    step, then steps until ``budget_s`` is spent and at least ``min_steps``
+    ran, or every decode step of the workload.  The cache's prompt positions
+    are zero except the first few: a decode step's cost does not depend on the
+    cache's values."""
     import torch
 
-    B, P = wl.batch, wl.prompt
-    ref.reset(B, P + wl.new_tokens)
+    B, P, N = wl.batch, wl.prompt, wl.new_tokens
+    ref.reset(B, P + N)
     g = torch.Generator().manual_seed(0)
     head = min(P, 64)
     for ck, cv in zip(ref.cache_k, ref.cache_v):
         ck[:, :, :head].copy_(torch.randn(ck[:, :, :head].shape, generator=g))
         cv[:, :, :head].copy_(torch.randn(cv[:, :, :head].shape, generator=g))
     tok = torch.tensor(wl.prompt_ids(), dtype=torch.int64)[:, -1:]
-    tok = ref.step(tok, P)  # warm
+    tok = ref.step(tok, P)  # warm: decode step 0
+    available = N - 2  # decode steps 1 .. N-2 (step k attends over P + k + 1 keys)
     steps, t0 = 0, time.perf_counter()
-    while True:
+    while steps < available:
         tok = ref.step(tok, P + 1 + steps)
         steps += 1
-        if time.perf_counter() - t0 > budget_s or P + 2 + steps >= P + wl.new_tokens:
+        if time.perf_counter() - t0 > budget_s and steps >= min(min_steps, available):
             break
     dt = time.perf_counter() - t0
     ref.cache_k = ref.cache_v = None
     cores = torch.get_num_threads()
+    whole = "every further decode step" if steps == available else f"{steps} decode steps"
     return {"value": round(B * steps / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "cpu": cpu_model(), "ms_per_step": round(dt / steps * 1e3, 1),
-            "sample": f"{steps} decode steps of {wl.name} (B={B}) at context {P + 2}..{P + 1 + steps} after one "
-                      f"warm step, on a pre-filled cache; the reference engine's eager CPU path restated in "
-                      f"PyTorch BF16 (oracle/ref_cpu_path.py: fused qkv and gate/up GEMMs, repeat-KV SDPA over "
-                      f"the full capacity with an additive mask), {cores} threads"}
+            "sample": f"{whole} of {wl.name} (B={B}) at context {P + 2}..{P + 1 + steps} after one "
+                      f"warm step, on a pre-filled cache at the workload's real shape; the reference engine's "
+                      f"eager CPU path restated in PyTorch BF16 (oracle/ref_cpu_path.py: fused qkv and gate/up "
+                      f"GEMMs, repeat-KV SDPA over the full capacity with an additive mask), {cores} threads"}
 
 
 def run_workload(eng, wl, K: int, W: int) -> dict:
@@ -290,7 +299,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--extra-configs", default="3,4",
+    ap.add_argument("--extra-configs", default="1,3,4,5",
                     help="comma-separated BASELINE configs reported beside the headline (empty: none)")
     ap.add_argument("--ckpt-dir", default=os.environ.get("Q3_CKPT_DIR", "/tmp/q3_seeded_qwen3_4b"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -330,7 +339,7 @@ def main() -> int:
         ref = RefCpuDecode(cfg, tensors)
         del tensors
         for wl in [head] + extras:
-            results[wl.number]["cpu_baseline"] = cpu_baseline(ref, wl, 20.0 if wl is head else 8.0)
+            results[wl.number]["cpu_baseline"] = cpu_baseline(ref, wl, 20.0 if wl is head else 6.0)
             log(f"{wl.name}: cpu baseline {results[wl.number]['cpu_baseline']}")
 
     r = results[head.number]

@@ -63,7 +63,7 @@ def replay_judge(model, input_ids, emitted, margin: float = 2.0) -> dict:
     logits = model.prefill(ids)
     short = np.zeros((N, B))
     for k in range(N):
-        lg = logits.float()
+        lg = logits.float().cpu()
         arg = lg.argmax(dim=-1)
         val = lg.gather(1, em[k].view(B, 1))[:, 0]
         short[k] = torch.where(arg == em[k], torch.zeros_like(val), lg.max(dim=-1).values - val).numpy()

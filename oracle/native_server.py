@@ -1,12 +1,21 @@
 """Native Qwen behind the contest's streaming protocol -- TEST INFRASTRUCTURE.
 
-The contest times native Qwen (Transformers' greedy loop) through the same
-pipe and clock as the candidate, and its TTFT/TPOT medians set the candidate's
-latency gates (reference QWEN_ENGINE_CONTRACT.md "What is measured").  Here
-native Qwen is the CPU oracle (``qwen3_cpu.Qwen3Oracle``, bit-identical to
-HF's CPU path on the seeded model), streamed one step at a time:
+The contest times native Qwen (Transformers' greedy loop on the judge's GPU)
+through the same pipe and clock as the candidate, and its TTFT/TPOT medians
+set the candidate's latency gates (reference QWEN_ENGINE_CONTRACT.md "What is
+measured", :94-96,125-133).  Two natives, streamed one step at a time:
 
-    python -m oracle.native_server MODEL_PATH BATCH PROMPT NEW
+  * ``--gpu``: the native the gates are measured against.  HF's forward op by
+    op, eagerly, on ``cuda:0`` in BF16: the CPU oracle's op sequence
+    (``qwen3_cpu.Qwen3Oracle``: separate q, k, v and gate, up projections as
+    torch GEMMs, RMSNorm and RoPE as elementwise torch ops, a preallocated
+    cache written in place) with attention as two batched torch GEMMs and a
+    softmax per KV head.  A plain greedy loop, no graph, no fused kernels, one
+    host sync per step to read the token, as HF's generate loop runs.
+  * default: the CPU oracle itself (bit-identical to HF's CPU path on the
+    seeded model), for hosts without a GPU.
+
+    python -m oracle.native_server MODEL_PATH BATCH PROMPT NEW [--gpu]
 
 Only tests use it, as the native side of ``starter_amd.protocol.run_workload``.
 """
@@ -19,6 +28,66 @@ import time
 import torch
 
 from oracle.qwen3_cpu import Qwen3Oracle, argmax_first
+
+
+def attention_bmm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                  start: int) -> torch.Tensor:
+    """GQA attention of T queries at positions start.. over keys 0..start+T-1,
+    causal, as two batched GEMMs per (sequence, KV head).
+
+    q ``[B, Hq, T, D]``; k, v ``[B, Hkv, L, D]`` views of the cache (L =
+    start + T).  Scores are computed as ``K . Q^T`` ([L, G*T] per KV head), so
+    that every batched product's right operand is a contiguous tensor (the
+    live V rows are copied, as HF's concatenating cache holds them): no
+    transposed view is ever a BF16 ``bmm`` operand.  Softmax in FP32 over the
+    keys, P rounded to BF16 before P.V, as SDPA's math path does."""
+    B, Hq, T, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    kf = k.reshape(B * Hkv, L, D)
+    vf = v.reshape(B * Hkv, L, D).contiguous()
+    qt = q.reshape(B * Hkv, G * T, D).transpose(1, 2).contiguous()      # [B*Hkv, D, G*T]
+    s = torch.bmm(kf, qt).float() * scale                              # [B*Hkv, L, G*T]
+    if T > 1:
+        keys = torch.arange(L, device=q.device).view(L, 1)
+        qpos = start + (torch.arange(G * T, device=q.device) % T).view(1, G * T)
+        s.masked_fill_(keys > qpos, float("-inf"))
+    p = torch.softmax(s, dim=1).to(q.dtype).transpose(1, 2).contiguous()  # [B*Hkv, G*T, L]
+    return torch.bmm(p, vf).view(B, Hq, T, D)
+
+
+class NativeGpu:
+    """The baseline greedy loop (reference tests/test_equivalence.py:72-86) on the GPU."""
+
+    def __init__(self, model_path: str, device: str = "cuda:0"):
+        from starter_amd.checkpoint import load_checkpoint
+        cfg, tensors = load_checkpoint(model_path)
+        self.VOCAB = cfg.vocab_size
+        self.model = Qwen3Oracle(cfg, tensors, torch.bfloat16, device=device)
+        self.model.attend = attention_bmm
+        del tensors
+
+    # The judge's interface (oracle.compare.replay_judge): reset / prefill / forward.
+    def reset(self, batch: int, capacity: int) -> None:
+        self.model.reset(batch, capacity)
+
+    def prefill(self, ids: torch.Tensor) -> torch.Tensor:
+        return self.model.prefill(ids.to(self.model.device))
+
+    def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
+        return self.model.forward(ids.to(self.model.device), start)
+
+    @torch.inference_mode()
+    def generate(self, input_ids, max_new_tokens: int):
+        ids = torch.tensor(input_ids, dtype=torch.int64, device=self.model.device)
+        B, P = ids.shape
+        self.model.reset(B, P + max_new_tokens)
+        logits = self.model.prefill(ids)
+        for step in range(max_new_tokens):
+            tok = argmax_first(logits)
+            yield tok.tolist()
+            if step + 1 < max_new_tokens:
+                logits = self.model.forward(tok.view(B, 1), P + step)
 
 
 class NativeCpu:
@@ -45,11 +114,15 @@ class NativeCpu:
 
 def main(argv) -> int:
     from starter_amd.protocol import serve
+    gpu = "--gpu" in argv
+    argv = [a for a in argv if a != "--gpu"]
     model_path, batch, prompt, new = argv[0], int(argv[1]), int(argv[2]), int(argv[3])
+    real_stdout = sys.stdout
+    sys.stdout = sys.stderr  # only protocol lines reach the pipe
     t0 = time.perf_counter()
-    native = NativeCpu(model_path)
+    native = NativeGpu(model_path) if gpu else NativeCpu(model_path)
     warm = [[(7 * r + 13 * t) % native.VOCAB for t in range(prompt)] for r in range(batch)]
-    serve(native, warm, new, load_s=time.perf_counter() - t0)
+    serve(native, warm, new, out=real_stdout, load_s=time.perf_counter() - t0)
     return 0
 
 

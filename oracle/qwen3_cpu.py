@@ -140,11 +140,16 @@ class Qwen3Oracle:
     reference ``tests/test_equivalence.py:25-27``).
     """
 
-    def __init__(self, cfg, tensors: dict, dtype=torch.bfloat16, threads: int | None = None):
+    def __init__(self, cfg, tensors: dict, dtype=torch.bfloat16, threads: int | None = None,
+                 device: str = "cpu"):
         if threads:
             torch.set_num_threads(threads)
         self.cfg = cfg
         self.dtype = dtype
+        #: The oracle runs on the CPU.  ``device`` exists for the test harness's
+        #: native comparator (``oracle/native_server.py``), which replays this
+        #: op sequence eagerly on a GPU to time it; parity never uses it.
+        self.device = torch.device(device)
         self.D = cfg.head_dim
         self.Hq = cfg.num_attention_heads
         self.Hkv = cfg.num_key_value_heads
@@ -152,7 +157,7 @@ class Qwen3Oracle:
         self.scale = cfg.head_dim ** -0.5
 
         def t(name):
-            return bf16_from_bits(tensors[name]).to(dtype)
+            return bf16_from_bits(tensors[name]).to(dtype).to(self.device)
 
         self.embed = t("model.embed_tokens.weight")
         self.lm_head = (self.embed if cfg.tie_word_embeddings
@@ -179,14 +184,17 @@ class Qwen3Oracle:
         #: The projection; tests swap in another summation order (see
         #: ``f32_linear``) to measure what reordering alone moves.
         self.linear = linear
+        #: The attention (``attention`` above); the GPU comparator swaps in its own.
+        self.attend = attention
 
     def reset(self, batch: int, capacity: int) -> None:
         """Fresh cache of ``capacity`` slots (reference ``engine/engine.py:843-862``)."""
-        self.cos, self.sin = rope_tables(self.cfg.rope_theta, self.D, max(capacity + 1, 4096),
-                                         self.dtype)
+        cos, sin = rope_tables(self.cfg.rope_theta, self.D, max(capacity + 1, 4096), self.dtype)
+        self.cos, self.sin = cos.to(self.device), sin.to(self.device)
         shape = (batch, self.Hkv, capacity, self.D)
-        self.cache_k = [torch.zeros(shape, dtype=self.dtype) for _ in self.layers]
-        self.cache_v = [torch.zeros(shape, dtype=self.dtype) for _ in self.layers]
+        self.cache_k = self.cache_v = None
+        self.cache_k = [torch.zeros(shape, dtype=self.dtype, device=self.device) for _ in self.layers]
+        self.cache_v = [torch.zeros(shape, dtype=self.dtype, device=self.device) for _ in self.layers]
 
     def block(self, x: torch.Tensor, i: int, start: int) -> torch.Tensor:
         """One ``Qwen3DecoderLayer`` (HF ``modeling_qwen3.py:294-323``, attention ``:241-280``)."""
@@ -205,8 +213,8 @@ class Qwen3Oracle:
         k = apply_rope(k.transpose(1, 2), cos, sin)
         self.cache_k[i][:, :, start:start + T] = k
         self.cache_v[i][:, :, start:start + T] = v.transpose(1, 2)
-        a = attention(q, self.cache_k[i][:, :, :start + T], self.cache_v[i][:, :, :start + T],
-                      self.scale, start)
+        a = self.attend(q, self.cache_k[i][:, :, :start + T], self.cache_v[i][:, :, :start + T],
+                        self.scale, start)
         a = a.transpose(1, 2).reshape(B, T, self.Hq * self.D)
         x = residual + lin(a, L["o"])
 
@@ -218,7 +226,7 @@ class Qwen3Oracle:
     @torch.inference_mode()
     def forward(self, ids: torch.Tensor, start: int) -> torch.Tensor:
         """Consume ``ids [B,T]`` at positions start..start+T-1; logits ``[B,V]`` of the last."""
-        x = F.embedding(ids, self.embed)
+        x = F.embedding(ids.to(self.device), self.embed)
         for i in range(len(self.layers)):
             x = self.block(x, i, start)
         x = rms_norm(x, self.final_norm, self.eps)

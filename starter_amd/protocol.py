@@ -17,7 +17,8 @@ Wire format (one JSON object per line, both directions):
   child -> client  {"ready": true, "load_s": s, "warmup_s": s}   after load + warmup
   client -> child  {"ids": [[...], ...], "new": N}                one sample
   child -> client  {"step": [id, ...]}                            N times, flushed each
-  child -> client  {"done": true, "peak_bytes": b, "device_bytes": b}
+  child -> client  {"done": true, "peak_bytes": b, "reserved_bytes": b, "used_bytes": b,
+                   "device_bytes": b}
   client -> child  {"quit": true}
 Anything the engine prints goes to stderr; stdout carries only these lines.
 
@@ -30,9 +31,11 @@ contest's limits to what it measured.
 from __future__ import annotations
 
 import json
+import queue
 import statistics
 import subprocess
 import sys
+import threading
 import time
 from dataclasses import dataclass, field
 
@@ -49,26 +52,36 @@ def _emit(out, obj) -> None:
     out.flush()
 
 
-def _memory() -> tuple[int, int]:
-    """(peak bytes the process reserved on the device, device bytes); 0s without a GPU."""
+def _memory() -> tuple[int, int, int]:
+    """(bytes torch's caching allocator has reserved at its peak, bytes in use on
+    the whole device now, device bytes); 0s without a GPU.  The device figure
+    (``hipMemGetInfo``: total - free) also holds what the allocator does not see
+    -- the HIP context, code objects, graph memory, a library's static device
+    arrays -- and anything else on the device."""
     try:
         import torch
         if torch.cuda.is_available():
-            return torch.cuda.max_memory_reserved(), torch.cuda.get_device_properties(0).total_memory
+            free, total = torch.cuda.mem_get_info(0)
+            return torch.cuda.max_memory_reserved(), total - free, total
     except Exception:  # noqa: BLE001 - a server without torch / GPU reports no memory
         pass
-    return 0, 0
+    return 0, 0, 0
 
 
 def serve(engine, warmup_ids: list[list[int]], warmup_new: int, inp=None, out=None,
           load_s: float = 0.0) -> None:
     """Child side: warm up on a prompt of the workload's shape, announce
-    readiness, then answer samples until told to quit (or stdin closes)."""
+    readiness, then answer samples until told to quit (or stdin closes).
+
+    Each sample's ``done`` line reports ``peak_bytes``: the larger of the
+    allocator's reserved peak and the device's used bytes, read after the
+    warmup and after every sample so far (``_memory``)."""
     inp = inp if inp is not None else sys.stdin
     out = out if out is not None else sys.stdout
     t0 = time.perf_counter()
     for _ in engine.generate(warmup_ids, warmup_new):
         pass
+    _, used_peak, _ = _memory()
     _emit(out, {"ready": True, "load_s": round(load_s, 3), "warmup_s": round(time.perf_counter() - t0, 3)})
     for line in inp:
         msg = json.loads(line)
@@ -76,8 +89,10 @@ def serve(engine, warmup_ids: list[list[int]], warmup_new: int, inp=None, out=No
             break
         for step in engine.generate(msg["ids"], msg["new"]):
             _emit(out, {"step": [int(t) for t in step]})
-        peak, device = _memory()
-        _emit(out, {"done": True, "peak_bytes": peak, "device_bytes": device})
+        reserved, used, device = _memory()
+        used_peak = max(used_peak, used)
+        _emit(out, {"done": True, "peak_bytes": max(reserved, used_peak), "reserved_bytes": reserved,
+                    "used_bytes": used_peak, "device_bytes": device})
 
 
 @dataclass
@@ -130,31 +145,53 @@ class ProtocolError(RuntimeError):
     pass
 
 
-def _read(proc, deadline: float) -> dict:
-    line = proc.stdout.readline()
-    if not line:
-        raise ProtocolError(f"the engine process ended (exit {proc.poll()}) before answering")
-    if time.perf_counter() > deadline:
-        raise ProtocolError("the engine process exceeded its time budget")
-    return json.loads(line)
+class _Lines:
+    """The child's stdout lines, read by a daemon thread into a queue, so that
+    the client can wait for the next one with a deadline (a child that hangs
+    or stops writing must not block the clock's owner)."""
+
+    def __init__(self, stream):
+        self.q: queue.Queue = queue.Queue()
+        threading.Thread(target=self._pump, args=(stream,), daemon=True).start()
+
+    def _pump(self, stream) -> None:
+        try:
+            for line in stream:
+                self.q.put(line)
+        finally:
+            self.q.put(None)
+
+    def get(self, proc, deadline: float, what: str) -> dict:
+        remaining = deadline - time.perf_counter()
+        try:
+            line = self.q.get(timeout=max(remaining, 0.0))
+        except queue.Empty:
+            raise ProtocolError(f"the engine process exceeded its time budget ({what})") from None
+        if line is None:
+            raise ProtocolError(f"the engine process ended (exit {proc.poll()}) before answering ({what})")
+        if time.perf_counter() > deadline:
+            raise ProtocolError(f"the engine process exceeded its time budget ({what})")
+        return json.loads(line)
 
 
 def run_workload(cmd: list[str], prompts: list[list[list[int]]], new_tokens: int, env=None,
-                 cwd=None) -> WorkloadRun:
+                 cwd=None, load_budget_s: float = LOAD_BUDGET_S,
+                 sample_budget_s: float = SAMPLE_BUDGET_S) -> WorkloadRun:
     """Client side: start ``cmd`` (a child that speaks this protocol), wait for
     it to load and warm up, then time each prompt's stream.  The clock is this
-    process's; the child's own claims are used only for its memory figures."""
+    process's; the child's own claims are used only for its memory figures.
+    A child that misses the load or a sample budget is killed and the run
+    raises ``ProtocolError``."""
     batch = len(prompts[0])
     proc = subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True, bufsize=1,
                             env=env, cwd=cwd)
+    lines = _Lines(proc.stdout)
     try:
         t0 = time.perf_counter()
-        hello = _read(proc, t0 + LOAD_BUDGET_S)
+        hello = lines.get(proc, t0 + load_budget_s, "load and warmup")
         if not hello.get("ready"):
             raise ProtocolError(f"expected the ready line, got {hello}")
         run = WorkloadRun(batch, new_tokens, hello.get("load_s", 0.0), hello.get("warmup_s", 0.0))
-        if time.perf_counter() - t0 > LOAD_BUDGET_S:
-            raise ProtocolError("load plus warmup exceeded 300 s")
         for ids in prompts:
             if len(ids) != batch:
                 raise ProtocolError("every sample of a workload has the same batch")
@@ -163,7 +200,7 @@ def run_workload(cmd: list[str], prompts: list[list[list[int]]], new_tokens: int
             proc.stdin.flush()
             steps, arrivals = [], []
             while True:
-                msg = _read(proc, start + SAMPLE_BUDGET_S)
+                msg = lines.get(proc, start + sample_budget_s, f"sample {len(run.samples)}")
                 if "step" in msg:
                     arrivals.append(time.perf_counter() - start)
                     steps.append(msg["step"])

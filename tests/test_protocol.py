@@ -12,7 +12,9 @@ from starter_amd import protocol
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 #: A child that speaks the protocol: first step after `first` seconds, then one
-#: every `every` seconds; `steps_off` emits that many extra (or fewer) steps.
+#: every `every` seconds; `steps_off` emits that many extra (or fewer) steps;
+#: `load` seconds pass before the warmup, and the step numbered `stall` (when
+#: >= 0) waits 60 s first (a hung engine).
 FAKE = """
 import sys, time
 sys.path.insert(0, {root!r})
@@ -20,19 +22,25 @@ from starter_amd.protocol import serve
 
 class Fake:
     VOCAB = 100
+    calls = 0
     def generate(self, ids, new):
+        Fake.calls += 1
         time.sleep({first})
         for k in range(new + {steps_off}):
             if k:
                 time.sleep({every})
+            if Fake.calls > 1 and k == {stall}:
+                time.sleep(60)
             yield [(r + k) % 100 for r in range(len(ids))]
 
+time.sleep({load})
 serve(Fake(), [[1, 2]], 2)
 """
 
 
-def fake_cmd(first=0.05, every=0.01, steps_off=0):
-    return [sys.executable, "-c", FAKE.format(root=str(ROOT), first=first, every=every, steps_off=steps_off)]
+def fake_cmd(first=0.05, every=0.01, steps_off=0, load=0.0, stall=-1):
+    return [sys.executable, "-c", FAKE.format(root=str(ROOT), first=first, every=every, steps_off=steps_off,
+                                              load=load, stall=stall)]
 
 
 def test_client_times_the_stream():
@@ -52,6 +60,41 @@ def test_client_times_the_stream():
 def test_wrong_step_count_is_an_error():
     with pytest.raises(protocol.ProtocolError, match="wrong stream shape"):
         protocol.run_workload(fake_cmd(steps_off=-1), [[[1, 2]]], 4)
+
+
+@pytest.mark.parametrize("load,stall", [(60.0, -1), (0.0, 2)], ids=["load", "mid_sample"])
+def test_silent_child_is_killed_at_its_budget(load, stall):
+    """A child that stops writing (during load, or in the middle of a sample's
+    stream) does not block the client: the read waits only until the budget,
+    the run raises, and the child is killed."""
+    import time
+
+    t0 = time.perf_counter()
+    with pytest.raises(protocol.ProtocolError, match="time budget"):
+        protocol.run_workload(fake_cmd(load=load, stall=stall), [[[1, 2]]], 4,
+                              load_budget_s=2.0, sample_budget_s=1.0)
+    assert time.perf_counter() - t0 < 20
+
+
+def test_native_attention_matches_oracle_attention():
+    """The GPU native's attention (two batched products per KV head, scores as
+    K . Q^T) against the oracle's SDPA, in float32 on the CPU: decode, a whole
+    causal prompt, and a later chunk over a cached prefix."""
+    import torch
+
+    from oracle import qwen3_cpu as oc
+    from oracle.native_server import attention_bmm
+
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, D, C = 2, 8, 2, 16, 40
+    for T, start in ((1, 17), (9, 0), (6, 11)):
+        q = torch.randn(B, Hq, T, D, generator=g)
+        ck = torch.randn(B, Hkv, C, D, generator=g)
+        cv = torch.randn(B, Hkv, C, D, generator=g)
+        k, v = ck[:, :, :start + T], cv[:, :, :start + T]
+        want = oc.attention(q, k, v, D ** -0.5, start)
+        got = attention_bmm(q, k, v, D ** -0.5, start)
+        assert torch.allclose(got, want, atol=1e-5, rtol=1e-5), (T, start)
 
 
 def test_gates():
