@@ -80,6 +80,10 @@ struct DecodeArgs {
     int Hq, Hkv, capacity, splits;
     float eps, scale;
     int B;  // sequences: the stride of one split of qkv_part [qkv_splits, B, ld_qkv]
+    // q|k|v as flagged words [B, ld_qkv] written by the same launch (QP 3),
+    // and the word a timed-out wait for them sets.
+    const uint32_t* qkv_x = nullptr;
+    int* err = nullptr;
 };
 
 // Elements idx and idx + 64 of sequence b's projected q|k|v row: BF16 from
@@ -89,7 +93,8 @@ struct DecodeArgs {
 // independent load in flight before it waits for any (vector memory counters
 // retire in order).  Up to QKV_FAST splits load at once; more take a loop.
 constexpr int QKV_FAST = 8;
-// QP: 0 = BF16 row, 1 = up to QKV_FAST split partials, 2 = more partials (loop).
+// QP: 0 = BF16 row, 1 = up to QKV_FAST split partials, 2 = more partials (loop),
+// 3 = flagged BF16 words from workgroups of the same launch (qkv_poll).
 template <int QP>
 struct QkvRaw {
     bf16_t blo, bhi;  // BF16 row (converted only when used, so no wait here)
@@ -117,7 +122,7 @@ __device__ __forceinline__ void qkv_issue(const DecodeArgs& a, int b, int idx, Q
 template <int QP>
 __device__ __forceinline__ void qkv_finish(const DecodeArgs& a, int b, int idx, const QkvRaw<QP>& r, float& lo,
                                            float& hi) {
-    if constexpr (QP == 0) {
+    if constexpr (QP == 0 || QP == 3) {
         lo = bf2f(r.blo);
         hi = bf2f(r.bhi);
         return;
@@ -141,6 +146,45 @@ __device__ __forceinline__ void qkv_finish(const DecodeArgs& a, int b, int idx, 
     lo = rbf(slo);
     hi = rbf(shi);
 }
+
+// QP 3: sequence b's q|k|v elements idx and idx + 64 for the three rows this
+// lane needs, re-read past the L2s until every word carries flag F (the
+// projection workgroups of the launch store them as they finish).  Bounded
+// (1 s): past it the wait sets *a.err and the payloads are used as they are.
+__device__ __forceinline__ void qkv_poll(const DecodeArgs& a, int b, int qidx, int kidx, int vidx, uint32_t F,
+                                         QkvRaw<3>& qr, QkvRaw<3>& kr, QkvRaw<3>& vr) {
+    const auto rs = q3x::rsrc(a.qkv_x);
+    const int base = 4 * b * a.ld_qkv;
+    const uint32_t Fs = F << 16;
+    q3x::SpinBound sb;
+    uint32_t w[6];
+    for (;;) {
+        const int idx[6] = {qidx, qidx + 64, kidx, kidx + 64, vidx, vidx + 64};
+#pragma unroll
+        for (int j = 0; j < 6; ++j) w[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, base + 4 * idx[j], 0, q3x::SC1);
+        uint32_t bad = 0;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) bad |= (w[j] ^ Fs) & 0xffff0000u;
+        if (__all(bad == 0)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (!sb.ok(q3x::SPIN_LIMIT)) {
+            if (a.err != nullptr && (threadIdx.x & 63) == 0)
+                __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    qr.blo = (bf16_t)(w[0] & 0xffffu);
+    qr.bhi = (bf16_t)(w[1] & 0xffffu);
+    kr.blo = (bf16_t)(w[2] & 0xffffu);
+    kr.bhi = (bf16_t)(w[3] & 0xffffu);
+    vr.blo = (bf16_t)(w[4] & 0xffffu);
+    vr.bhi = (bf16_t)(w[5] & 0xffffu);
+}
+
+// No work between the attention prologue's loads and its first wait.
+struct NoMid {
+    __device__ __forceinline__ void operator()() const {}
+};
 
 // One 32-key block of K and V rows in registers: load j covers keys 4j..4j+3
 // whole, lane l holding chunk (l % 16) ^ (key & 15) of key 4j + l / 16, which is
@@ -195,8 +239,13 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // normalised output is written here.  Eight waves (one workgroup per CU, 128 KB
 // of tiles) when the grid leaves CUs idle and every wave still gets a block:
 // twice the loads in flight per (sequence, KV head).
-template <int WAVES, int QP>
-__device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kvh, int b, uint32_t* xbuf, uint32_t F) {
+//
+// mid() runs once every load of the prologue is in flight and before any wait
+// for one (every wave of the workgroup calls it): the fused q|k|v projection
+// computes its rows there while this unit's first key block streams in.
+template <int WAVES, int QP, class Mid = NoMid>
+__device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kvh, int b, uint32_t* xbuf, uint32_t F,
+                                          Mid mid = Mid()) {
     static_assert(WAVES == 4 || WAVES == 8, "four or eight waves");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -244,7 +293,15 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
     const bool owner = !bad_pos && begin <= pos && pos < end;
     const Pair16 cr = pair16(a.cos_t + (int64_t)pos * D, lane), sr = pair16(a.sin_t + (int64_t)pos * D, lane);
     __builtin_amdgcn_sched_barrier(0);
+    mid();
+    if constexpr (QP == 3) qkv_poll(a, b, qidx, kidx, vidx, F, qr, kr, vr);
 
+    // The appended key (wave 0) and value (wave 1) of the owning split, stored
+    // to the cache at the end: a store counts against the same in-order vector
+    // memory counter as the key block's loads, so storing it here would make
+    // the first block's wait also wait for the store's completion.  No other
+    // workgroup reads row pos this step, and this one substitutes it from LDS.
+    uint32_t app_lo = 0, app_hi = 0;
     if (begin < end) {
         // Query head kvh*4 + w: RMSNorm + RoPE into LDS.
         uint32_t lo, hi;
@@ -262,9 +319,8 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             norm_rope_pair(k_lo, k_hi, kg, cr, sr, a.eps, lo, hi);
             knew[lane] = (bf16_t)lo;
             knew[lane + 64] = (bf16_t)hi;
-            bf16_t* dst = a.cache_k + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
-            dst[lane] = (bf16_t)lo;
-            dst[lane + 64] = (bf16_t)hi;
+            app_lo = lo;
+            app_hi = hi;
         }
         if (owner && w == 1) {
             float v_lo, v_hi;
@@ -272,9 +328,8 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             const bf16_t v0 = (bf16_t)f2bf(v_lo), v1 = (bf16_t)f2bf(v_hi);
             vnew[lane] = v0;
             vnew[lane + 64] = v1;
-            bf16_t* dst = a.cache_v + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
-            dst[lane] = v0;
-            dst[lane + 64] = v1;
+            app_lo = v0;
+            app_hi = v1;
         }
     }
     __syncthreads();
@@ -333,20 +388,35 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             for (int i = 0; i < 4; ++i) macc[w * WSTRIDE + n * D + 16 * dm + 4 * g + i] = st.acc[dm][i];
     }
     __syncthreads();
-    for (int e = tid; e < GROUP * D; e += WAVES * 64) {
-        const int h = e / D, d = e % D;
+    // Thread tid folds elements e = tid + i * 64 WAVES (head e / D, d = e % D)
+    // over the waves that held keys.  Every LDS value is requested before any
+    // is used (one round trip, not one per wave), and the empty waves are
+    // skipped by selects; the fold's operations and order are unchanged.
+    constexpr int EPT = GROUP * D / (WAVES * 64);
+    static_assert(EPT * WAVES * 64 == GROUP * D, "whole elements per thread");
+    float wm[EPT][WAVES], wl[EPT][WAVES], wa[EPT][WAVES];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + i * WAVES * 64, h = e / D, d = e % D;
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) {
+            wm[i][ww] = mm[ww][h];
+            wl[i][ww] = ll[ww][h];
+            wa[i][ww] = macc[ww * WSTRIDE + h * D + d];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + i * WAVES * 64, h = e / D, d = e % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < WAVES; ++ww)
-            if (ll[ww][h] > 0.f) M = fmaxf(M, mm[ww][h]);
+        for (int ww = 0; ww < WAVES; ++ww) M = wl[i][ww] > 0.f ? fmaxf(M, wm[i][ww]) : M;
         float sacc = 0.f, sl = 0.f;
 #pragma unroll
         for (int ww = 0; ww < WAVES; ++ww) {
-            if (ll[ww][h] > 0.f) {
-                const float wt = expf(mm[ww][h] - M);
-                sacc += macc[ww * WSTRIDE + h * D + d] * wt;
-                sl += ll[ww][h] * wt;
-            }
+            const float wt = expf(wm[i][ww] - M);
+            sacc = wl[i][ww] > 0.f ? sacc + wa[i][ww] * wt : sacc;
+            sl = wl[i][ww] > 0.f ? sl + wl[i][ww] * wt : sl;
         }
         const int qh = kvh * GROUP + h;
         const int64_t p = ((int64_t)b * a.Hq + qh) * a.splits + split;
@@ -371,6 +441,11 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             a.part_ml[2 * p + 1] = sl;
         }
     }
+    if (owner && w < 2) {  // the KV append (fused.py:553-638)
+        bf16_t* dst = (w == 0 ? a.cache_k : a.cache_v) + (((int64_t)b * a.Hkv + kvh) * a.capacity + pos) * D;
+        dst[lane] = (bf16_t)app_lo;
+        dst[lane + 64] = (bf16_t)app_hi;
+    }
 }
 
 template <int WAVES, int QP>
@@ -378,35 +453,18 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_decode_kernel(Deco
     attn_unit<WAVES, QP>(a, blockIdx.x, blockIdx.y, blockIdx.z, nullptr, 0);
 }
 
-// Attention and split merge in one launch (several splits, small grids).  The
-// first splits * Hkv * B workgroups are the attention units above (the wave
-// count q3_attn_decode would use, so the partials are the same bits); each
-// stores its partial record -- 128 accumulators and (max, sum), every FP32 as
-// two flagged words -- past the XCD-private L2.  The last Hq * B / (WAVES / 2)
-// workgroups merge WAVES / 2 heads each: they re-read the records of every split until all
-// words carry this (position, layer)'s flag, then fold them exactly as
-// attn_merge_kernel does.  The whole grid is resident at once (the launcher
-// caps it), so a merging workgroup never waits on a unit that cannot start;
-// its wait is still bounded (1 s), after which it writes zeros and sets *err.
-template <int WAVES, int QP>
-__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(DecodeArgs a, uint32_t* xbuf, int layer,
-                                                                          int* err) {
+// The exchange flag of (position, layer): never 0, so zeroed words never match.
+__device__ __forceinline__ uint32_t step_flag(int pos_raw, int layer) {
+    return 1u + ((uint32_t)pos_raw * 64u + (uint32_t)layer) % 65535u;
+}
+
+// Merge workgroup mi of a fused launch: heads HPW mi .. HPW mi + HPW - 1 of
+// sequence b; thread t takes (head t / 128, d = t % 128).
+template <int WAVES>
+__device__ __forceinline__ void merge_unit(const DecodeArgs& a, int mi, const uint32_t* xbuf, uint32_t F, int* err) {
     constexpr int HPW = WAVES / 2;  // heads per merging workgroup (128 threads each)
-    const int n_att = a.splits * a.Hkv * a.B;
-    const int n_mrg = a.Hq / HPW * a.B;
-    const int pos_raw = (int)*a.pos;
-    const uint32_t F = 1u + ((uint32_t)pos_raw * 64u + (uint32_t)layer) % 65535u;
-    const int bid = blockIdx.x;
-    if (bid < n_att) {
-        const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
-        attn_unit<WAVES, QP>(a, split, kvh, b, xbuf, F);
-        return;
-    }
-    if (bid >= n_att + n_mrg) return;
-    // Merge: heads HPW mi .. HPW mi + HPW - 1 of sequence b; thread t takes
-    // (head t / 128, d = t % 128).
     constexpr int CH = 16;
-    const int mi = bid - n_att, hp = a.Hq / HPW;
+    const int hp = a.Hq / HPW;
     const int b = mi / hp, h = HPW * (mi % hp) + (int)(threadIdx.x >> 7), d = threadIdx.x & 127;
     const int S = a.splits;
     const auto rs = q3x::rsrc(xbuf);
@@ -466,6 +524,216 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(Decod
     }
     const uint32_t y = f2bf(l_run > 0.f ? acc / l_run : 0.f);
     a.out[((int64_t)b * a.Hq + h) * D + d] = (bf16_t)y;
+}
+
+// Attention and split merge in one launch (several splits, small grids).  The
+// first splits * Hkv * B workgroups are the attention units above (the wave
+// count q3_attn_decode would use, so the partials are the same bits); each
+// stores its partial record -- 128 accumulators and (max, sum), every FP32 as
+// two flagged words -- past the XCD-private L2.  The last Hq * B / (WAVES / 2)
+// workgroups merge WAVES / 2 heads each: they re-read the records of every split until all
+// words carry this (position, layer)'s flag, then fold them exactly as
+// attn_merge_kernel does.  The whole grid is resident at once (the launcher
+// caps it), so a merging workgroup never waits on a unit that cannot start;
+// its wait is still bounded (1 s), after which it writes zeros and sets *err.
+template <int WAVES, int QP>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_fused_kernel(DecodeArgs a, uint32_t* xbuf, int layer,
+                                                                          int* err) {
+    const int n_att = a.splits * a.Hkv * a.B;
+    const int n_mrg = a.Hq / (WAVES / 2) * a.B;
+    const uint32_t F = step_flag((int)*a.pos, layer);
+    const int bid = blockIdx.x;
+    if (bid < n_att) {
+        const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
+        attn_unit<WAVES, QP>(a, split, kvh, b, xbuf, F);
+        return;
+    }
+    if (bid < n_att + n_mrg) merge_unit<WAVES>(a, bid - n_att, xbuf, F, err);
+}
+
+// ------------------------------------- q|k|v projection and attention, one launch
+//
+// At 1-2 rows the layer's first two steps -- the q|k|v projection (RMSNorm
+// prologue, reference engine/engine.py:431-450,665-690) and decode attention
+// with its split merge -- run as one grid.  Every workgroup computes a few
+// weight rows per wave of the projection and stores each output as a flagged
+// word (BF16 payload, this (position, layer)'s flag) past the L2s; the first
+// splits * Hkv * B workgroups are also attention units, which put their first
+// key block's loads in flight before the projection and then wait only for the
+// 768 words of their own KV head (q3x exchange, no counters or fences); the
+// next Hq / 2 * B workgroups merge the splits as in attn_fused_kernel.  The
+// projection's arithmetic and order are those of gemv_dot2_kernel (X_NORM /
+// X_EMBED_NORM, EPI_STORE), so the words carry the bits q3_gemv stores.
+
+// Projection rows per wave: RA on the attention workgroups, RO on the others.
+// A CU streams at most ~27 GB/s, so rows are dealt to even out each CU's
+// bytes: an attention workgroup also streams its split's keys (96 keys of K
+// and V = 48 KB, about ten weight rows of 5 KB), so at one row of input with
+// K = 2560 it takes 5 rows per wave and the others 7 (N = 6144 at 16 splits:
+// 128 + 128 workgroups); otherwise 6 and 6.
+
+struct QkvGemvArgs {
+    const bf16_t* x;       // X_NORM: rows to normalise [M, ldx]; X_EMBED_NORM: the embedding table
+    int ldx;
+    const int64_t* ids;    // X_EMBED_NORM: token ids [M]
+    const bf16_t* norm_w;  // RMSNorm gain [K]
+    float eps;
+    bf16_t* resid_out;     // X_EMBED_NORM: the embedding rows are copied here [M, K]
+    const bf16_t* w;       // weights [N, K]
+    int N;
+    uint32_t* qx;          // outputs as flagged words [M, N]
+};
+
+__device__ __forceinline__ float dot8v(u32x4_t a, u32x4_t b, float c) {
+    c = dot2(a.x, b.x, c);
+    c = dot2(a.y, b.y, c);
+    c = dot2(a.z, b.z, c);
+    c = dot2(a.w, b.w, c);
+    return c;
+}
+
+// Rows row0 .. row0 + R - 1 of the projection (this wave's; rows past N are
+// neither stored nor read past the matrix) for M input rows, K = 512 KU: the
+// input rows (and gain) are requested, then every weight load, then the norm
+// runs while the weights stream.  Every wave of the workgroup calls it (it
+// synchronises the workgroup).
+template <int M, int KU, int XMODE, int R>
+__device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_t F, bf16_t* xs, float (*red)[M]) {
+    constexpr int K = 512 * KU;
+    constexpr int XC = (64 * KU + 255) / 256;  // 16-byte input chunks per thread
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    u32x4_t xv[XC][M], gv[XC];
+    const bf16_t* src[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        if constexpr (XMODE == Q3_X_EMBED_NORM) src[m] = g.x + g.ids[m] * (int64_t)K;
+        else src[m] = g.x + (int64_t)m * g.ldx;
+    }
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = min(tid + j * 256, 64 * KU - 1);  // past the row: a duplicate, never used
+        gv[j] = *reinterpret_cast<const u32x4_t*>(g.norm_w + c * 8);
+#pragma unroll
+        for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(src[m] + c * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional weight loads (a row past the last re-reads the last row
+    // and is not stored), all in flight before the norm waits.
+    const bf16_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = g.w + (int64_t)min(row0 + r, g.N - 1) * K + lane * 8;
+    u32x4_t wv[R][KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow[r] + u * 512));
+    __builtin_amdgcn_sched_barrier(0);
+
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ss[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = tid + j * 256;
+        if (c < 64 * KU) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const u32x4_t v = xv[j][m];
+                if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
+                    *reinterpret_cast<u32x4_t*>(g.resid_out + (int64_t)m * K + c * 8) = v;
+                float t = ss[m];
+                t += bflo(v.x) * bflo(v.x); t += bfhi(v.x) * bfhi(v.x);
+                t += bflo(v.y) * bflo(v.y); t += bfhi(v.y) * bfhi(v.y);
+                t += bflo(v.z) * bflo(v.z); t += bfhi(v.z) * bfhi(v.z);
+                t += bflo(v.w) * bflo(v.w); t += bfhi(v.w) * bfhi(v.w);
+                ss[m] = t;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float t = wave_sum(ss[m]);
+        if (lane == 0) red[wave][m] = t;
+    }
+    __syncthreads();
+    float inv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) inv[m] = inv_rms((red[0][m] + red[1][m]) + (red[2][m] + red[3][m]), K, g.eps);
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = tid + j * 256;
+        if (c < 64 * KU) {
+            const u32x4_t gg = gv[j];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                u32x4_t v = xv[j][m];
+                const float im = inv[m];
+                v.x = pack2(norm_elem(bflo(v.x), im, bflo(gg.x)), norm_elem(bfhi(v.x), im, bfhi(gg.x)));
+                v.y = pack2(norm_elem(bflo(v.y), im, bflo(gg.y)), norm_elem(bfhi(v.y), im, bfhi(gg.y)));
+                v.z = pack2(norm_elem(bflo(v.z), im, bflo(gg.z)), norm_elem(bfhi(v.z), im, bfhi(gg.z)));
+                v.w = pack2(norm_elem(bflo(v.w), im, bflo(gg.w)), norm_elem(bfhi(v.w), im, bfhi(gg.w)));
+                *reinterpret_cast<u32x4_t*>(xs + m * K + c * 8) = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const u32x4_t xc = *reinterpret_cast<const u32x4_t*>(xs + m * K + lane * 8 + u * 512);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][m] = dot8v(wv[r][u], xc, acc[r][m]);
+        }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = wave_sum(acc[r][m]);
+    // Lane r * M + m stores output (row0 + r, m).
+    if (lane < R * M && row0 + lane / M < g.N) {
+        const int r = lane / M, m = lane % M;
+        float v = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm)
+                if (rr == r && mm == m) v = acc[rr][mm];
+        q3x::st_coh32(g.qx + (int64_t)m * g.N + row0 + r, q3x::word(f2bf(v), F));
+    }
+}
+
+// Grid: max(projection workgroups, attention + merge workgroups), four waves
+// each, all resident at once (the launcher checks), so every wait is for a
+// workgroup that is running; each wait is still bounded (1 s, then *err).
+template <int M, int KU, int XMODE, int RA, int RO>
+__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeArgs a, uint32_t* xbuf, int layer,
+                                                         int n_gemv) {
+    __shared__ __align__(16) bf16_t xs[M * 512 * KU];
+    __shared__ float red[4][M];
+    const int n_att = a.splits * a.Hkv * a.B;
+    const int n_mrg = a.Hq / 2 * a.B;
+    const uint32_t F = step_flag((int)*a.pos, layer);
+    const int bid = blockIdx.x, wave = threadIdx.x >> 6;
+    const auto gemv = [&]() {
+        if (bid >= n_gemv) return;
+        if (bid < n_att) qkv_rows<M, KU, XMODE, RA>(g, (bid * 4 + wave) * RA, F, xs, red);
+        else qkv_rows<M, KU, XMODE, RO>(g, n_att * 4 * RA + ((bid - n_att) * 4 + wave) * RO, F, xs, red);
+    };
+    if (bid < n_att) {
+        const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
+        attn_unit<4, 3>(a, split, kvh, b, xbuf, F, gemv);
+        return;
+    }
+    gemv();
+    if (bid < n_att + n_mrg) merge_unit<4>(a, bid - n_att, xbuf, F, a.err);
 }
 
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
@@ -891,6 +1159,118 @@ extern "C" int q3_attn_decode_fused(const bf16_t* qkv, int ld_qkv, const float* 
     return attn_fused_launch(qkv, ld_qkv, qkv_part, qkv_splits, q_norm_w, k_norm_w, cos_table, sin_table, pos,
                              cache_k, cache_v, xbuf, out, B, Hq, Hkv, capacity, splits, layer, eps, scale, err,
                              q3_attn_fused_grid(B, Hq, Hkv, capacity, splits), stream);
+}
+
+// ------------------------------------- q|k|v projection + attention launcher
+
+// Launch plan of the fused kernel: the row split (RA rows per wave on the
+// attention workgroups, RO on the others), the projection's workgroup count
+// and the grid.
+struct QaPlan {
+    int ra = 0, ro = 0, n_gemv = 0, grid = 0;
+};
+
+static QaPlan qa_plan(int B, int Hq, int Hkv, int splits, int K) {
+    const int N = (Hq + 2 * Hkv) * D;
+    const int n_att = B * splits * Hkv, n_rest = B * (splits * Hkv + Hq / 2);
+    QaPlan p;
+    if (B == 1 && K == 2560 && n_att * 4 * 5 <= N) {
+        p.ra = 5;
+        p.ro = 7;
+    } else {
+        p.ra = p.ro = 6;
+    }
+    const int left = N - n_att * 4 * p.ra;  // rows for the other workgroups
+    p.n_gemv = left <= 0 ? (N + 4 * p.ra - 1) / (4 * p.ra) : n_att + (left + 4 * p.ro - 1) / (4 * p.ro);
+    p.grid = p.n_gemv > n_rest ? p.n_gemv : n_rest;
+    return p;
+}
+
+template <int M, int KU, int XMODE, int RA, int RO>
+static const void* qkv_attn_fn() {
+    return reinterpret_cast<const void*>(qkv_attn_kernel<M, KU, XMODE, RA, RO>);
+}
+
+// The fused kernel for (rows, K, input mode, row split), or null outside what
+// it is built for.
+static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra) {
+    const bool emb = x_mode == Q3_X_EMBED_NORM;
+    if (x_mode != Q3_X_NORM && !emb) return nullptr;
+    if (ra == 5) {
+        if (M != 1 || K != 2560) return nullptr;
+        return emb ? qkv_attn_fn<1, 5, Q3_X_EMBED_NORM, 5, 7>() : qkv_attn_fn<1, 5, Q3_X_NORM, 5, 7>();
+    }
+#define Q3_QA_M(MV)                                                                                           \
+    case MV:                                                                                                  \
+        if (K == 2560)                                                                                        \
+            return emb ? qkv_attn_fn<MV, 5, Q3_X_EMBED_NORM, 6, 6>() : qkv_attn_fn<MV, 5, Q3_X_NORM, 6, 6>(); \
+        if (K == 512)                                                                                         \
+            return emb ? qkv_attn_fn<MV, 1, Q3_X_EMBED_NORM, 6, 6>() : qkv_attn_fn<MV, 1, Q3_X_NORM, 6, 6>(); \
+        return nullptr;
+    switch (M) {
+        Q3_QA_M(1)
+        Q3_QA_M(2)
+    }
+#undef Q3_QA_M
+    return nullptr;
+}
+
+// Workgroups of the fused kernel resident at once on the current device, for
+// both input modes of (rows, K, row split) (0 if unknown).  Cached per device
+// and kernel.
+static int qkv_attn_resident(int M, int K, int ra) {
+    constexpr int MAX_DEV = 64;
+    static int cached[MAX_DEV][2][2][2];  // 0 = not yet asked; -1 = unknown
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    int& c = cached[dev][M - 1][K == 2560 ? 1 : 0][ra == 5 ? 1 : 0];
+    if (c != 0) return c > 0 ? c : 0;
+    int cus = 0, per = 1 << 30;
+    bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
+    for (int xm : {Q3_X_NORM, Q3_X_EMBED_NORM}) {
+        const void* fn = qkv_attn_kernel_for(M, K, xm, ra);
+        int n = 0;
+        ok = ok && fn != nullptr && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) == hipSuccess;
+        per = n < per ? n : per;
+    }
+    ok = ok && per >= 1;
+    c = ok ? per * cus : -1;
+    return ok ? per * cus : 0;
+}
+
+extern "C" int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K) {
+    if (B < 1 || B > 2 || (K != 512 && K != 2560) || Hkv < 1 || Hq != GROUP * Hkv) return 0;
+    if (q3_attn_fused_grid(B, Hq, Hkv, capacity, splits) == 0) return 0;
+    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K);
+    return p.grid <= qkv_attn_resident(B, K, p.ra) ? p.grid : 0;
+}
+
+extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* ids, const bf16_t* norm_w,
+                           float eps, bf16_t* resid_out, const bf16_t* w, int K, uint32_t* qkv_x,
+                           const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
+                           const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
+                           uint32_t* xbuf, bf16_t* out, int B, int Hq, int Hkv, int capacity, int splits, int layer,
+                           float scale, int* err, hipStream_t stream) {
+    const int grid = q3_qkv_attn_grid(B, Hq, Hkv, capacity, splits, K);
+    const bool emb = x_mode == Q3_X_EMBED_NORM;
+    if (grid == 0 || (x_mode != Q3_X_NORM && !emb) || layer < 0 || layer >= 64 || !x || !norm_w || !w ||
+        !qkv_x || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !pos || !cache_k || !cache_v || !xbuf ||
+        !out || (emb ? (!ids || !resid_out) : (ldx < K || (ldx % 8) != 0)) ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(norm_w) |
+          reinterpret_cast<uintptr_t>(xbuf)) & 15) ||
+        (reinterpret_cast<uintptr_t>(qkv_x) & 3) || (emb && (reinterpret_cast<uintptr_t>(resid_out) & 15)))
+        return (int)hipErrorInvalidValue;
+    const int N = (Hq + 2 * Hkv) * D;
+    const QkvGemvArgs g{x, ldx, ids, norm_w, eps, resid_out, w, N, qkv_x};
+    DecodeArgs a{nullptr, N, nullptr, 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
+                 nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B, qkv_x, err};
+    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K);
+    const void* fn = qkv_attn_kernel_for(B, K, x_mode, p.ra);
+    int n_gemv = p.n_gemv;
+    void* args[] = {(void*)&g, (void*)&a, (void*)&xbuf, (void*)&layer, (void*)&n_gemv};
+    (void)hipGetLastError();
+    const hipError_t rc = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+    return rc != hipSuccess ? (int)rc : (int)hipGetLastError();
 }
 
 extern "C" int q3_attn_merge(const float* part_acc, const float* part_ml, bf16_t* out, int B, int Hq,

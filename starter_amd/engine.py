@@ -82,6 +82,11 @@ SKINNY_BATCH_MAX = 64
 FUSED_ATTENTION = os.environ.get("Q3_FUSED_ATTENTION", "1") != "0"
 FUSED_ATTENTION_MAX_LAYERS = 64
 
+#: At 1-2 rows, also the q|k|v projection in that launch (``q3_qkv_attn``):
+#: attention starts streaming its keys while the projection runs and waits
+#: only for its own KV head's rows.  False keeps the projection separate.
+QKV_ATTENTION = os.environ.get("Q3_QKV_ATTENTION", "1") != "0"
+
 #: The contest judge's tie margin (reference QWEN_ENGINE_CONTRACT.md
 #: "tieMarginLogits", currently 2.0): an emitted token must be the replayed
 #: argmax or within this many logits of it.
@@ -285,6 +290,11 @@ class Engine:
         self.attn_x = torch.zeros(words, dtype=torch.int32, device=self.device)
         self.attn_err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.small = B <= GEMV_BATCH_MAX
+        # The q|k|v projection in the same launch, its outputs passed as
+        # flagged words (cleared with the attention's).
+        self.qkv_attn = (QKV_ATTENTION and self.small and self.attn_fused and
+                         call("q3_qkv_attn_grid", B, self.HEADS, Hkv, capacity, self.splits, H) > 0)
+        self.qkv_x = torch.zeros(B * self.qkv_size if self.qkv_attn else 4, dtype=torch.int32, device=self.device)
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
         # Split-K workspace of the MFMA decode projections: every projection's
         # partials, [splits, B, N] FP32, one consumer at a time.
@@ -370,7 +380,15 @@ class Engine:
         resid, qkv, attn, act, nbuf = (_ptr(self.resid), _ptr(self.qkv_buf), _ptr(self.attn_out),
                                        _ptr(self.act), _ptr(self.nbuf))
         for i, L in enumerate(self.layers):
-            if self.small:
+            if self.qkv_attn:
+                first = i == 0
+                call("q3_qkv_attn", _lib.X_EMBED_NORM if first else _lib.X_NORM, _ptr(self.embed) if first else resid,
+                     H, tok if first else None, _ptr(L["in_ln"]), self.EPS, resid if first else None,
+                     _ptr(L["qkv"]), H, _ptr(self.qkv_x), _ptr(L["q_norm"]), _ptr(L["k_norm"]),
+                     _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
+                     vc0 + i * layer_stride, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i, self.SCALE,
+                     _ptr(self.attn_err), s)
+            elif self.small:
                 if i == 0:
                     call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
                          resid, _ptr(L["qkv"]), B, self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size,
@@ -386,7 +404,9 @@ class Engine:
                 else:
                     call("q3_rmsnorm", resid, H, _ptr(L["in_ln"]), nbuf, H, B, H, self.EPS, s)
                 self._proj(nbuf, H, L["qkv"], self.qkv_size, H, _lib.EPI_STORE, qkv, self.qkv_size)
-            self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride, vc0 + i * layer_stride)
+            if not self.qkv_attn:
+                self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride,
+                                vc0 + i * layer_stride)
             if self.small:
                 call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
                      B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, 0, s)
@@ -497,10 +517,12 @@ class Engine:
         _log(f"decode graph captured (batch={self.batch}, splits={self.splits})")
 
     def _clear_exchange(self) -> None:
-        """Zero the fused attention's exchange words and timeout word on the
-        decode stream.  Its flags are derived from (position, layer), so words
-        left by an earlier call at the same positions would read as fresh."""
+        """Zero the fused launches' exchange words (attention partials, q|k|v
+        rows) and timeout word on the decode stream.  Their flags are derived
+        from (position, layer), so words left by an earlier call at the same
+        positions would read as fresh."""
         self.attn_x.zero_()
+        self.qkv_x.zero_()
         self.attn_err.zero_()
 
     def _begin_decode(self, logits: torch.Tensor, seq_len: int) -> None:
@@ -524,8 +546,8 @@ class Engine:
         rebuilds it."""
         if self.attn_fused and int(self.attn_err.cpu()[0]):
             self.graph_key_reset()
-            raise RuntimeError("the fused attention launch did not complete: a merge workgroup waited "
-                               "past its time bound")
+            raise RuntimeError("the fused attention launch did not complete: a workgroup waited for "
+                               "another's words past its time bound")
 
     # -------------------------------------------------------------- prefill
 

@@ -206,6 +206,32 @@ def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, bat
     check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
 
 
+@pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700)])
+def test_qkv_attention_launch_matches_separate_projection(tile_engine, tile_ckpt, batch, prompt):
+    """At 1-2 rows the q|k|v projection joins the fused attention launch
+    (q3_qkv_attn): the same bits as the projection launched on its own, at every
+    step of trace_logits and generate, across repeated calls."""
+    saved = engine_mod.QKV_ATTENTION
+    cfg, _ = load_checkpoint(tile_ckpt)
+    rng = np.random.Generator(np.random.PCG64(950 + batch))
+    ids = rng.integers(0, cfg.vocab_size, (batch, prompt)).tolist()
+    runs = {}
+    try:
+        for joined in (True, False):
+            engine_mod.QKV_ATTENTION = joined
+            steps, logits = tile_engine.trace_logits(ids, 8)
+            assert tile_engine.qkv_attn == joined and tile_engine.attn_fused
+            tokens = list(tile_engine.generate(ids, 8))
+            assert tile_engine.qkv_attn == joined
+            again = list(tile_engine.generate(ids, 8))
+            assert int(tile_engine.attn_err.cpu()[0]) == 0
+            runs[joined] = (steps, logits, tokens, again)
+    finally:
+        engine_mod.QKV_ATTENTION = saved
+    assert torch.equal(runs[True][1], runs[False][1])
+    assert runs[True][0] == runs[False][0] == runs[True][2] == runs[True][3] == runs[False][2]
+
+
 def test_batch_rows_are_independent(tiny_engine):
     """A row's tokens do not depend on the other rows of the batch (bit-identical)."""
     rng = np.random.Generator(np.random.PCG64(3))

@@ -850,6 +850,103 @@ def test_attn_decode_fused_rejects_layers_past_its_flag():
     assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and err.item() == 0
 
 
+@pytest.mark.parametrize("B,Hkv,K,C,pos,splits,embed", [
+    (1, 8, 2560, 1536, 1100, 16, False),   # config 2's shape: 16 splits of 96 keys
+    (1, 8, 2560, 1536, 1535, 12, True),    # last slot, layer 0's embedding prologue
+    (2, 8, 2560, 700, 255, 4, False),
+    (2, 8, 2560, 900, 640, 5, True),
+    (1, 8, 2560, 300, 0, 2, False),        # first position: the new key is the only one
+    (1, 8, 2560, 64, 63, 2, False),
+    (1, 2, 512, 300, 200, 3, True),        # the tile test model's widths
+    (2, 2, 512, 700, 650, 6, False)])
+def test_qkv_attn_matches_projection_then_fused_attention(B, Hkv, K, C, pos, splits, embed):
+    """q3_qkv_attn == q3_gemv (X_NORM / X_EMBED_NORM, EPI_STORE) then
+    q3_attn_decode_fused, bit for bit: attention output, both caches and the
+    embedding rows copied to the residual, over several layers' flags, and
+    again after the exchange words are zeroed at a repeated (position, layer)."""
+    Hq, D = 4 * Hkv, 128
+    N = (Hq + 2 * Hkv) * D
+    assert call("q3_qkv_attn_grid", B, Hq, Hkv, C, splits, K) > 0
+    qw = dv((1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16))
+    kw = dv((1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16))
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    cos, sin = dv(cos), dv(sin)
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    posd = dv(torch.tensor([pos]))
+    V = 1000
+    table = dv(rnd((V, K), 0.5, 6))
+    ids = dv(torch.randint(0, V, (B,), generator=torch.Generator().manual_seed(7)))
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
+    xbuf2 = torch.zeros_like(xbuf)
+    qx = torch.zeros(B * N, dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for layer, seed in ((0, 11), (1, 12), (0, 13)):
+        if layer == 0 and seed == 13:
+            xbuf.zero_()  # the same (position, layer) as the first round
+            xbuf2.zero_()
+            qx.zero_()
+        x = dv(rnd((B, K), 1.5, seed))
+        g = dv((1 + rnd((K,), 0.2, seed + 50).float()).to(torch.bfloat16))
+        w = dv(rnd((N, K), 0.05, seed + 100))
+        xm = _lib.X_EMBED_NORM if embed else _lib.X_NORM
+        src = table if embed else x
+        outs, caches, resids = [], [], []
+        for fused in (False, True):
+            ckd, cvd = dv(ck), dv(cv)
+            out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+            resid = torch.zeros(B, K, dtype=torch.bfloat16, device=DEV)
+            if fused:
+                call("q3_qkv_attn", xm, P(src), K, P(ids) if embed else None, P(g), 1e-6,
+                     P(resid) if embed else None, P(w), K, P(qx), P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd),
+                     P(cvd), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
+            else:
+                qkv = torch.empty(B, N, dtype=torch.bfloat16, device=DEV)
+                gemv(xm, src, K, w, B, N, K, _lib.EPI_STORE, qkv, N, ids=ids if embed else None, norm_w=g,
+                     resid_out=resid if embed else None)
+                call("q3_attn_decode_fused", P(qkv), N, None, 0, P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd),
+                     P(cvd), P(xbuf2), P(out), B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5, P(err), S())
+            torch.cuda.synchronize()
+            outs.append(out.cpu())
+            caches.append((ckd.cpu(), cvd.cpu()))
+            resids.append(resid.cpu())
+        assert torch.equal(outs[0], outs[1]), (layer, seed)
+        assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+        assert torch.equal(resids[0], resids[1])
+        # Every projected row reached the exchange words with this step's flag.
+        flag = 1 + (pos * 64 + layer) % 65535
+        words = qx.cpu().view(torch.int32).numpy().view(np.uint32)
+        assert (words >> 16 == flag).all()
+    assert err.item() == 0
+
+
+def test_qkv_attn_refuses_what_it_is_not_built_for():
+    """Three rows, other widths and layers past the flag's field are refused
+    before anything is enqueued."""
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 2560) > 0
+    assert call("q3_qkv_attn_grid", 3, 32, 8, 1536, 6, 2560) == 0
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 4096) == 0
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 1, 2560) == 0   # one split: no fused attention
+    Hq, Hkv, D, B, C, splits, K = 32, 8, 128, 1, 1536, 16, 2560
+    N = (Hq + 2 * Hkv) * D
+    x = torch.zeros(B, K, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(N, K, dtype=torch.bfloat16, device=DEV)
+    gain = torch.ones(K, dtype=torch.bfloat16, device=DEV)
+    cos, sin = oc.rope_tables(5e6, D, C + 1)
+    cos, sin = dv(cos), dv(sin)
+    posd = dv(torch.tensor([5]))
+    ck = torch.zeros(B, Hkv, C, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
+    qx = torch.zeros(B * N, dtype=torch.int32, device=DEV)
+    out = torch.full((B, Hq * D), 7.0, dtype=torch.bfloat16, device=DEV)
+    for layer, xm in ((64, _lib.X_NORM), (-1, _lib.X_NORM), (3, _lib.X_PLAIN)):
+        with pytest.raises(RuntimeError):
+            call("q3_qkv_attn", xm, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain), P(cos),
+                 P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, D ** -0.5, None, S())
+    torch.cuda.synchronize()
+    assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and int(qx.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("B,C,pos,qsplits", [(1, 300, 200, 1), (5, 700, 650, 3), (16, 1000, 999, 6),
                                               # configs 5 and 4: qkv from the skinny projection's partials
                                               (8, 16512, 16500, 5), (64, 2176, 2100, 5)])
