@@ -247,20 +247,29 @@ int q3_attn_xbuf_words(int B, int Hq, int splits);
  * flagged words qkv_x [B, N] uint32 (BF16 payload, the (*pos, layer) flag of
  * xbuf); each unit waits only for its own KV head's rows, with its first key
  * block already in flight.  Bit for bit the same out, cache rows and resid_out
- * as q3_gemv + q3_attn_decode_fused.  The caller zeroes qkv_x and xbuf before
- * positions can repeat (a new prompt); eps is both norms' epsilon.  Applies
- * when q3_qkv_attn_grid(B, Hq, Hkv, capacity, splits, K) > 0 (what
- * q3_attn_fused_grid admits, and a grid resident at once).  A wait past 1 s
- * sets *err = 1 (err may be NULL).  Replaces reference engine/engine.py:665-736's
- * first half of _block -- _linear(qkv) (:431-450), _norm_rope_pair + KV append
- * (:458-462, fused.py:553-638) and _sdpa (:263-280) -- with one launch. */
+ * as q3_gemv + q3_attn_decode_fused.
+ * With w_o != NULL (B = 1, o [K, Hq * 128] with Hq * 128 = 4096 at K = 2560 or
+ * 1024 at K = 512) the o projection and its residual join run in the same
+ * launch: resid_out [K] += bf16(attention . w_oT), the bits of q3_gemv
+ * (X_PLAIN, EPI_RESID); the attention output goes to it as flagged words o_x
+ * [Hq * 128] uint32 (16-byte aligned) and out may be NULL.  In X_EMBED_NORM
+ * mode the join starts from the embedding row (resid_out is then written once,
+ * by the join).
+ * The caller zeroes qkv_x, xbuf and o_x before positions can repeat (a new
+ * prompt); eps is both norms' epsilon.  Applies when q3_qkv_attn_grid(B, Hq,
+ * Hkv, capacity, splits, K, w_o != NULL) > 0 (what q3_attn_fused_grid admits,
+ * and a grid resident at once).  A wait past 1 s sets *err = 1 (err may be
+ * NULL).  Replaces reference engine/engine.py:665-736's first half of _block --
+ * _linear(qkv) (:431-450), _norm_rope_pair + KV append (:458-462,
+ * fused.py:553-638), _sdpa (:263-280), _linear(o) and the residual add of
+ * _add_norm (:452-456) -- with one launch. */
 int q3_qkv_attn(int x_mode, const uint16_t *x, int ldx, const int64_t *ids, const uint16_t *norm_w,
                 float eps, uint16_t *resid_out, const uint16_t *w, int K, uint32_t *qkv_x,
                 const uint16_t *q_norm_w, const uint16_t *k_norm_w, const uint16_t *cos_table,
                 const uint16_t *sin_table, const int64_t *pos, uint16_t *cache_k, uint16_t *cache_v,
-                uint32_t *xbuf, uint16_t *out, int B, int Hq, int Hkv, int capacity, int splits, int layer,
-                float scale, int *err, hipStream_t stream);
-int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K);
+                uint32_t *xbuf, uint16_t *out, const uint16_t *w_o, uint32_t *o_x, int B, int Hq, int Hkv,
+                int capacity, int splits, int layer, float scale, int *err, hipStream_t stream);
+int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K, int with_o);
 
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
  * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /

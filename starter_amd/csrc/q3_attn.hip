@@ -84,6 +84,9 @@ struct DecodeArgs {
     // and the word a timed-out wait for them sets.
     const uint32_t* qkv_x = nullptr;
     int* err = nullptr;
+    // Fused launches with the o projection: the merged output as flagged
+    // words [B, Hq * 128] (out may then be null).
+    uint32_t* o_x = nullptr;
 };
 
 // Elements idx and idx + 64 of sequence b's projected q|k|v row: BF16 from
@@ -523,7 +526,8 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int mi, const ui
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint32_t y = f2bf(l_run > 0.f ? acc / l_run : 0.f);
-    a.out[((int64_t)b * a.Hq + h) * D + d] = (bf16_t)y;
+    if (a.out != nullptr) a.out[((int64_t)b * a.Hq + h) * D + d] = (bf16_t)y;
+    if (a.o_x != nullptr) q3x::st_coh32(a.o_x + ((int64_t)b * a.Hq + h) * D + d, q3x::word(y, F));
 }
 
 // Attention and split merge in one launch (several splits, small grids).  The
@@ -641,7 +645,7 @@ __device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const u32x4_t v = xv[j][m];
-                if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0)
+                if (XMODE == Q3_X_EMBED_NORM && blockIdx.x == 0 && g.resid_out != nullptr)
                     *reinterpret_cast<u32x4_t*>(g.resid_out + (int64_t)m * K + c * 8) = v;
                 float t = ss[m];
                 t += bflo(v.x) * bflo(v.x); t += bfhi(v.x) * bfhi(v.x);
@@ -710,13 +714,120 @@ __device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_
     }
 }
 
-// Grid: max(projection workgroups, attention + merge workgroups), four waves
-// each, all resident at once (the launcher checks), so every wait is for a
-// workgroup that is running; each wait is still bounded (1 s, then *err).
-template <int M, int KU, int XMODE, int RA, int RO>
-__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeArgs a, uint32_t* xbuf, int layer,
-                                                         int n_gemv) {
-    __shared__ __align__(16) bf16_t xs[M * 512 * KU];
+// The o projection with its residual join inside the same launch (one row of
+// input): resid[n] = bf16(resid[n] + bf16(sum_k W_o[n, k] * attn[k])), attn
+// being the merged attention output the merge workgroups store as flagged
+// words.  Arithmetic and order are those of gemv_dot2_kernel (X_PLAIN from
+// LDS, EPI_RESID), so resid gets the bits q3_gemv would store.
+struct OprojArgs {
+    const bf16_t* w;       // W_o [N, K], K = 512 KUO
+    int N;                 // = the hidden size (the residual's width)
+    bf16_t* resid;         // [N]: read, joined, written
+    const bf16_t* table;   // X_EMBED_NORM launches: the embedding table, whose row ids[0] is the
+    const int64_t* ids;    //   residual the join starts from (nothing else writes resid in this launch)
+    const uint32_t* ox;    // the merged attention output as flagged words [K]
+};
+// o rows per wave: QO_RN on the workgroups that are neither attention units
+// nor merging ones (idle once their q|k|v rows are stored, so their o weights
+// stream while the attention runs), QO_RA on attention workgroups for the rows
+// left (their loads issued when the unit is done).
+constexpr int QO_RN = 4, QO_RA = 2;
+
+// This wave's o weight rows row0 .. row0 + R - 1, requested (rows past N
+// re-read the last row and are not stored).
+template <int R, int KUO>
+__device__ __forceinline__ void o_issue(const OprojArgs& o, int row0, u32x4_t (&wo)[R][KUO]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < KUO; ++u)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wo[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
+                o.w + (int64_t)min(row0 + r, o.N - 1) * (512 * KUO) + lane * 8 + u * 512));
+}
+
+// Wait for the merged output (a few words first, one per merging workgroup,
+// then every word until all carry flag F), stage it in LDS, finish this
+// wave's rows.  Every wave of the workgroup calls it.  Bounded (1 s, then
+// *err and the payloads as they are).
+template <int XMODE, int R, int KUO>
+__device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32x4_t (&wo)[R][KUO], uint32_t F,
+                                         int* err, bf16_t* xo) {
+    constexpr int K = 512 * KUO;
+    constexpr int WPT = K / 256;  // words per thread
+    static_assert(WPT % 4 == 0, "whole 16-byte loads");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const auto rs = q3x::rsrc(o.ox);
+    const uint32_t Fs = F << 16;
+    q3x::SpinBound sb;
+    bool ok = true;
+    // One word per 256 (a merging workgroup's share) until those are current.
+    for (;;) {
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (min(lane, K / 256 - 1) * 256 + 255), 0,
+                                                                q3x::SC1);
+        if (__all(((v ^ Fs) & 0xffff0000u) == 0)) break;
+        __builtin_amdgcn_s_sleep(2);
+        if (!sb.ok(q3x::SPIN_LIMIT)) {
+            ok = false;
+            break;
+        }
+    }
+    u32x4_t ow[WPT / 4];
+    for (;;) {
+#pragma unroll
+        for (int j = 0; j < WPT / 4; ++j) ow[j] = q3x::ld_coh(rs, 16 * (tid * (WPT / 4) + j));
+        uint32_t bad = 0;
+#pragma unroll
+        for (int j = 0; j < WPT / 4; ++j) bad |= q3x::unflagged(ow[j], Fs);
+        if (__all(bad == 0) || !ok) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (!sb.ok(q3x::SPIN_LIMIT)) {
+            ok = false;
+            break;
+        }
+    }
+    if (!ok && err != nullptr && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int j = 0; j < WPT / 4; ++j) {
+        const u32x4_t v = ow[j];
+        reinterpret_cast<uint32_t*>(xo)[tid * (WPT / 2) + 2 * j] = q3x::bfpair(v.x, v.y);
+        reinterpret_cast<uint32_t*>(xo)[tid * (WPT / 2) + 2 * j + 1] = q3x::bfpair(v.z, v.w);
+    }
+    __syncthreads();
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int u = 0; u < KUO; ++u) {
+        const u32x4_t xc = *reinterpret_cast<const u32x4_t*>(xo + lane * 8 + u * 512);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8v(wo[r][u], xc, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane < R && row0 + lane < o.N) {
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r == lane) v = acc[r];
+        const int n = row0 + lane;
+        const bf16_t old = XMODE == Q3_X_EMBED_NORM ? o.table[o.ids[0] * (int64_t)o.N + n] : o.resid[n];
+        o.resid[n] = (bf16_t)f2bf(bf2f(old) + rbf(v));
+    }
+}
+
+// Grid: max(projection workgroups, attention + merge workgroups + the o
+// projection's other workgroups), four waves each, all resident at once (the
+// launcher checks), so every wait is for a workgroup that is running; each
+// wait is still bounded (1 s, then *err).  With the o projection (KUO > 0, one
+// row of input): workgroup n_att + n_mrg + j (j < n_on) takes o rows 16 j ..
+// 16 j + 15, and attention workgroup i (i < n_oa) rows 16 n_on + 8 i .. + 7.
+template <int M, int KU, int XMODE, int RA, int RO, int KUO>
+__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeArgs a, OprojArgs o, uint32_t* xbuf,
+                                                         int layer, int n_gemv, int n_on, int n_oa) {
+    static_assert(KUO == 0 || M == 1, "the fused o projection takes one row");
+    constexpr int XS = M * 512 * KU > 512 * KUO ? M * 512 * KU : 512 * KUO;
+    __shared__ __align__(16) bf16_t xs[XS];
     __shared__ float red[4][M];
     const int n_att = a.splits * a.Hkv * a.B;
     const int n_mrg = a.Hq / 2 * a.B;
@@ -730,10 +841,30 @@ __global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeA
     if (bid < n_att) {
         const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
         attn_unit<4, 3>(a, split, kvh, b, xbuf, F, gemv);
+        if constexpr (KUO > 0) {
+            if (bid < n_oa) {
+                const int row0 = 16 * n_on + (bid * 4 + wave) * QO_RA;
+                u32x4_t wo[QO_RA][KUO];
+                o_issue<QO_RA, KUO>(o, row0, wo);
+                o_finish<XMODE, QO_RA, KUO>(o, row0, wo, F, a.err, xs);
+            }
+        }
         return;
     }
     gemv();
-    if (bid < n_att + n_mrg) merge_unit<4>(a, bid - n_att, xbuf, F, a.err);
+    if (bid < n_att + n_mrg) {
+        merge_unit<4>(a, bid - n_att, xbuf, F, a.err);
+        return;
+    }
+    if constexpr (KUO > 0) {
+        const int j = bid - n_att - n_mrg;
+        if (j < n_on) {
+            const int row0 = (j * 4 + wave) * QO_RN;
+            u32x4_t wo[QO_RN][KUO];
+            o_issue<QO_RN, KUO>(o, row0, wo);
+            o_finish<XMODE, QO_RN, KUO>(o, row0, wo, F, a.err, xs);
+        }
+    }
 }
 
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
@@ -1164,15 +1295,15 @@ extern "C" int q3_attn_decode_fused(const bf16_t* qkv, int ld_qkv, const float* 
 // ------------------------------------- q|k|v projection + attention launcher
 
 // Launch plan of the fused kernel: the row split (RA rows per wave on the
-// attention workgroups, RO on the others), the projection's workgroup count
-// and the grid.
+// attention workgroups, RO on the others), the projection's workgroup count,
+// the o projection's workgroup count (0 without it) and the grid.
 struct QaPlan {
-    int ra = 0, ro = 0, n_gemv = 0, grid = 0;
+    int ra = 0, ro = 0, n_gemv = 0, n_on = 0, n_oa = 0, grid = 0;
 };
 
-static QaPlan qa_plan(int B, int Hq, int Hkv, int splits, int K) {
+static QaPlan qa_plan(int B, int Hq, int Hkv, int splits, int K, bool with_o) {
     const int N = (Hq + 2 * Hkv) * D;
-    const int n_att = B * splits * Hkv, n_rest = B * (splits * Hkv + Hq / 2);
+    const int n_att = B * splits * Hkv, n_mrg = B * Hq / 2, n_rest = n_att + n_mrg;
     QaPlan p;
     if (B == 1 && K == 2560 && n_att * 4 * 5 <= N) {
         p.ra = 5;
@@ -1183,52 +1314,61 @@ static QaPlan qa_plan(int B, int Hq, int Hkv, int splits, int K) {
     const int left = N - n_att * 4 * p.ra;  // rows for the other workgroups
     p.n_gemv = left <= 0 ? (N + 4 * p.ra - 1) / (4 * p.ra) : n_att + (left + 4 * p.ro - 1) / (4 * p.ro);
     p.grid = p.n_gemv > n_rest ? p.n_gemv : n_rest;
+    if (with_o) {
+        // o rows (the hidden size K): 16 per workgroup past the merging ones,
+        // the rest 8 per attention workgroup, else more workgroups.
+        const int need = (K + 4 * QO_RN - 1) / (4 * QO_RN);
+        p.n_on = p.grid - n_rest < need ? p.grid - n_rest : need;
+        const int left_o = K - 4 * QO_RN * p.n_on;
+        p.n_oa = left_o <= 0 ? 0 : (left_o + 4 * QO_RA - 1) / (4 * QO_RA);
+        if (p.n_oa > n_att) {
+            p.n_oa = 0;
+            p.n_on = need;
+            p.grid = n_rest + need;
+        }
+    }
     return p;
 }
 
-template <int M, int KU, int XMODE, int RA, int RO>
+template <int M, int KU, int XMODE, int RA, int RO, int KUO>
 static const void* qkv_attn_fn() {
-    return reinterpret_cast<const void*>(qkv_attn_kernel<M, KU, XMODE, RA, RO>);
+    return reinterpret_cast<const void*>(qkv_attn_kernel<M, KU, XMODE, RA, RO, KUO>);
 }
 
-// The fused kernel for (rows, K, input mode, row split), or null outside what
-// it is built for.
-static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra) {
+// The fused kernel for (rows, K, input mode, row split, o width / 512), or
+// null outside what it is built for.
+static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra, int kuo) {
     const bool emb = x_mode == Q3_X_EMBED_NORM;
     if (x_mode != Q3_X_NORM && !emb) return nullptr;
-    if (ra == 5) {
-        if (M != 1 || K != 2560) return nullptr;
-        return emb ? qkv_attn_fn<1, 5, Q3_X_EMBED_NORM, 5, 7>() : qkv_attn_fn<1, 5, Q3_X_NORM, 5, 7>();
-    }
-#define Q3_QA_M(MV)                                                                                           \
-    case MV:                                                                                                  \
-        if (K == 2560)                                                                                        \
-            return emb ? qkv_attn_fn<MV, 5, Q3_X_EMBED_NORM, 6, 6>() : qkv_attn_fn<MV, 5, Q3_X_NORM, 6, 6>(); \
-        if (K == 512)                                                                                         \
-            return emb ? qkv_attn_fn<MV, 1, Q3_X_EMBED_NORM, 6, 6>() : qkv_attn_fn<MV, 1, Q3_X_NORM, 6, 6>(); \
-        return nullptr;
-    switch (M) {
-        Q3_QA_M(1)
-        Q3_QA_M(2)
-    }
-#undef Q3_QA_M
+#define Q3_QA(MV, KUV, RAV, ROV, KUOV)                                                                     \
+    if (M == MV && K == 512 * KUV && ra == RAV && kuo == KUOV)                                             \
+        return emb ? qkv_attn_fn<MV, KUV, Q3_X_EMBED_NORM, RAV, ROV, KUOV>()                               \
+                   : qkv_attn_fn<MV, KUV, Q3_X_NORM, RAV, ROV, KUOV>();
+    Q3_QA(1, 5, 5, 7, 0)
+    Q3_QA(1, 5, 6, 6, 0)
+    Q3_QA(2, 5, 6, 6, 0)
+    Q3_QA(1, 1, 6, 6, 0)
+    Q3_QA(2, 1, 6, 6, 0)
+    Q3_QA(1, 5, 5, 7, 8)  // Qwen3-4B: o is [2560, 4096]
+    Q3_QA(1, 5, 6, 6, 8)
+    Q3_QA(1, 1, 6, 6, 2)  // the 512-wide test model: o is [512, 1024]
+#undef Q3_QA
     return nullptr;
 }
 
 // Workgroups of the fused kernel resident at once on the current device, for
-// both input modes of (rows, K, row split) (0 if unknown).  Cached per device
-// and kernel.
-static int qkv_attn_resident(int M, int K, int ra) {
+// both input modes (0 if unknown).  Cached per device and kernel.
+static int qkv_attn_resident(int M, int K, int ra, int kuo) {
     constexpr int MAX_DEV = 64;
-    static int cached[MAX_DEV][2][2][2];  // 0 = not yet asked; -1 = unknown
+    static int cached[MAX_DEV][2][2][2][3];  // 0 = not yet asked; -1 = unknown
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
-    int& c = cached[dev][M - 1][K == 2560 ? 1 : 0][ra == 5 ? 1 : 0];
+    int& c = cached[dev][M - 1][K == 2560 ? 1 : 0][ra == 5 ? 1 : 0][kuo == 0 ? 0 : kuo == 2 ? 1 : 2];
     if (c != 0) return c > 0 ? c : 0;
     int cus = 0, per = 1 << 30;
     bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
     for (int xm : {Q3_X_NORM, Q3_X_EMBED_NORM}) {
-        const void* fn = qkv_attn_kernel_for(M, K, xm, ra);
+        const void* fn = qkv_attn_kernel_for(M, K, xm, ra, kuo);
         int n = 0;
         ok = ok && fn != nullptr && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) == hipSuccess;
         per = n < per ? n : per;
@@ -1238,36 +1378,53 @@ static int qkv_attn_resident(int M, int K, int ra) {
     return ok ? per * cus : 0;
 }
 
-extern "C" int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K) {
+// o width / 512 of the fused o projection (0: not built for this shape).
+static int qkv_attn_kuo(int B, int Hq, int K) {
+    if (B != 1) return 0;
+    const int ko = Hq * D;
+    return (K == 2560 && ko == 4096) ? 8 : (K == 512 && ko == 1024) ? 2 : 0;
+}
+
+extern "C" int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K, int with_o) {
     if (B < 1 || B > 2 || (K != 512 && K != 2560) || Hkv < 1 || Hq != GROUP * Hkv) return 0;
+    const int kuo = with_o ? qkv_attn_kuo(B, Hq, K) : 0;
+    if (with_o && kuo == 0) return 0;
     if (q3_attn_fused_grid(B, Hq, Hkv, capacity, splits) == 0) return 0;
-    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K);
-    return p.grid <= qkv_attn_resident(B, K, p.ra) ? p.grid : 0;
+    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K, with_o != 0);
+    return p.grid <= qkv_attn_resident(B, K, p.ra, kuo) ? p.grid : 0;
 }
 
 extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* ids, const bf16_t* norm_w,
                            float eps, bf16_t* resid_out, const bf16_t* w, int K, uint32_t* qkv_x,
                            const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
                            const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
-                           uint32_t* xbuf, bf16_t* out, int B, int Hq, int Hkv, int capacity, int splits, int layer,
-                           float scale, int* err, hipStream_t stream) {
-    const int grid = q3_qkv_attn_grid(B, Hq, Hkv, capacity, splits, K);
+                           uint32_t* xbuf, bf16_t* out, const bf16_t* w_o, uint32_t* o_x, int B, int Hq, int Hkv,
+                           int capacity, int splits, int layer, float scale, int* err, hipStream_t stream) {
+    const bool with_o = w_o != nullptr;
+    const int grid = q3_qkv_attn_grid(B, Hq, Hkv, capacity, splits, K, with_o ? 1 : 0);
     const bool emb = x_mode == Q3_X_EMBED_NORM;
     if (grid == 0 || (x_mode != Q3_X_NORM && !emb) || layer < 0 || layer >= 64 || !x || !norm_w || !w ||
         !qkv_x || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !pos || !cache_k || !cache_v || !xbuf ||
-        !out || (emb ? (!ids || !resid_out) : (ldx < K || (ldx % 8) != 0)) ||
+        (emb ? (!ids || !resid_out) : (ldx < K || (ldx % 8) != 0)) ||
+        (with_o ? (!o_x || !resid_out || (reinterpret_cast<uintptr_t>(w_o) & 15) ||
+                   (reinterpret_cast<uintptr_t>(o_x) & 15))
+                : !out) ||
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(norm_w) |
           reinterpret_cast<uintptr_t>(xbuf)) & 15) ||
         (reinterpret_cast<uintptr_t>(qkv_x) & 3) || (emb && (reinterpret_cast<uintptr_t>(resid_out) & 15)))
         return (int)hipErrorInvalidValue;
     const int N = (Hq + 2 * Hkv) * D;
-    const QkvGemvArgs g{x, ldx, ids, norm_w, eps, resid_out, w, N, qkv_x};
+    // With the o projection, resid_out is the residual it joins; the embedding
+    // rows are not copied to it first (the join reads them from the table).
+    const QkvGemvArgs g{x, ldx, ids, norm_w, eps, with_o ? nullptr : resid_out, w, N, qkv_x};
     DecodeArgs a{nullptr, N, nullptr, 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
-                 nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B, qkv_x, err};
-    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K);
-    const void* fn = qkv_attn_kernel_for(B, K, x_mode, p.ra);
-    int n_gemv = p.n_gemv;
-    void* args[] = {(void*)&g, (void*)&a, (void*)&xbuf, (void*)&layer, (void*)&n_gemv};
+                 nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B, qkv_x, err, with_o ? o_x : nullptr};
+    const OprojArgs o{w_o, K, with_o ? resid_out : nullptr, emb ? x : nullptr, ids, o_x};
+    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K, with_o);
+    const void* fn = qkv_attn_kernel_for(B, K, x_mode, p.ra, with_o ? qkv_attn_kuo(B, Hq, K) : 0);
+    int n_gemv = p.n_gemv, n_on = p.n_on, n_oa = p.n_oa;
+    void* args[] = {(void*)&g, (void*)&a, (void*)&o,     (void*)&xbuf,
+                    (void*)&layer, (void*)&n_gemv, (void*)&n_on, (void*)&n_oa};
     (void)hipGetLastError();
     const hipError_t rc = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
     return rc != hipSuccess ? (int)rc : (int)hipGetLastError();

@@ -84,7 +84,9 @@ FUSED_ATTENTION_MAX_LAYERS = 64
 
 #: At 1-2 rows, also the q|k|v projection in that launch (``q3_qkv_attn``):
 #: attention starts streaming its keys while the projection runs and waits
-#: only for its own KV head's rows.  False keeps the projection separate.
+#: only for its own KV head's rows; at one row the o projection and its
+#: residual join too (their weights stream while the attention runs).  False
+#: keeps the projections separate.
 QKV_ATTENTION = os.environ.get("Q3_QKV_ATTENTION", "1") != "0"
 
 #: The contest judge's tie margin (reference QWEN_ENGINE_CONTRACT.md
@@ -293,8 +295,11 @@ class Engine:
         # The q|k|v projection in the same launch, its outputs passed as
         # flagged words (cleared with the attention's).
         self.qkv_attn = (QKV_ATTENTION and self.small and self.attn_fused and
-                         call("q3_qkv_attn_grid", B, self.HEADS, Hkv, capacity, self.splits, H) > 0)
+                         call("q3_qkv_attn_grid", B, self.HEADS, Hkv, capacity, self.splits, H, 0) > 0)
+        self.qkv_attn_o = (self.qkv_attn and
+                           call("q3_qkv_attn_grid", B, self.HEADS, Hkv, capacity, self.splits, H, 1) > 0)
         self.qkv_x = torch.zeros(B * self.qkv_size if self.qkv_attn else 4, dtype=torch.int32, device=self.device)
+        self.o_x = torch.zeros(B * self.q_size if self.qkv_attn_o else 4, dtype=torch.int32, device=self.device)
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
         # Split-K workspace of the MFMA decode projections: every projection's
         # partials, [splits, B, N] FP32, one consumer at a time.
@@ -381,13 +386,14 @@ class Engine:
                                        _ptr(self.act), _ptr(self.nbuf))
         for i, L in enumerate(self.layers):
             if self.qkv_attn:
-                first = i == 0
+                first, with_o = i == 0, self.qkv_attn_o
                 call("q3_qkv_attn", _lib.X_EMBED_NORM if first else _lib.X_NORM, _ptr(self.embed) if first else resid,
-                     H, tok if first else None, _ptr(L["in_ln"]), self.EPS, resid if first else None,
+                     H, tok if first else None, _ptr(L["in_ln"]), self.EPS, resid if first or with_o else None,
                      _ptr(L["qkv"]), H, _ptr(self.qkv_x), _ptr(L["q_norm"]), _ptr(L["k_norm"]),
                      _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                     vc0 + i * layer_stride, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i, self.SCALE,
-                     _ptr(self.attn_err), s)
+                     vc0 + i * layer_stride, _ptr(self.attn_x), None if with_o else attn,
+                     _ptr(L["o"]) if with_o else None, _ptr(self.o_x) if with_o else None,
+                     B, Hq, Hkv, C, self.splits, i, self.SCALE, _ptr(self.attn_err), s)
             elif self.small:
                 if i == 0:
                     call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
@@ -408,8 +414,9 @@ class Engine:
                 self._attention(i, L, (qkv, self.qkv_size, None, 0), kc0 + i * layer_stride,
                                 vc0 + i * layer_stride)
             if self.small:
-                call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
-                     B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, 0, s)
+                if not self.qkv_attn_o:
+                    call("q3_gemv", _lib.X_PLAIN, attn, self.q_size, None, None, 0.0, None, _ptr(L["o"]),
+                         B, H, self.q_size, _lib.EPI_RESID, resid, H, None, None, None, None, None, 0, s)
                 call("q3_gemv", _lib.X_NORM, resid, H, None, _ptr(L["post_ln"]), self.EPS, None,
                      _ptr(L["gate_up"]), B, 2 * I, H, _lib.EPI_SWIGLU, act, I, None, None, None, None, None, 0, s)
                 call("q3_gemv", _lib.X_PLAIN, act, I, None, None, 0.0, None, _ptr(L["down"]),
@@ -518,11 +525,12 @@ class Engine:
 
     def _clear_exchange(self) -> None:
         """Zero the fused launches' exchange words (attention partials, q|k|v
-        rows) and timeout word on the decode stream.  Their flags are derived
+        rows, attention output) and timeout word on the decode stream.  Their flags are derived
         from (position, layer), so words left by an earlier call at the same
         positions would read as fresh."""
         self.attn_x.zero_()
         self.qkv_x.zero_()
+        self.o_x.zero_()
         self.attn_err.zero_()
 
     def _begin_decode(self, logits: torch.Tensor, seq_len: int) -> None:

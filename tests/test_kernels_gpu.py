@@ -862,11 +862,15 @@ def test_attn_decode_fused_rejects_layers_past_its_flag():
 def test_qkv_attn_matches_projection_then_fused_attention(B, Hkv, K, C, pos, splits, embed):
     """q3_qkv_attn == q3_gemv (X_NORM / X_EMBED_NORM, EPI_STORE) then
     q3_attn_decode_fused, bit for bit: attention output, both caches and the
-    embedding rows copied to the residual, over several layers' flags, and
-    again after the exchange words are zeroed at a repeated (position, layer)."""
+    embedding rows copied to the residual; at one row also with the o
+    projection in the launch == that then q3_gemv (X_PLAIN, EPI_RESID) on the
+    residual.  Over several layers' flags, and again after the exchange words
+    are zeroed at a repeated (position, layer)."""
     Hq, D = 4 * Hkv, 128
-    N = (Hq + 2 * Hkv) * D
-    assert call("q3_qkv_attn_grid", B, Hq, Hkv, C, splits, K) > 0
+    N, KO = (Hq + 2 * Hkv) * D, Hq * D
+    assert call("q3_qkv_attn_grid", B, Hq, Hkv, C, splits, K, 0) > 0
+    with_o = call("q3_qkv_attn_grid", B, Hq, Hkv, C, splits, K, 1) > 0
+    assert with_o == (B == 1)
     qw = dv((1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16))
     kw = dv((1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16))
     cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
@@ -876,56 +880,66 @@ def test_qkv_attn_matches_projection_then_fused_attention(B, Hkv, K, C, pos, spl
     V = 1000
     table = dv(rnd((V, K), 0.5, 6))
     ids = dv(torch.randint(0, V, (B,), generator=torch.Generator().manual_seed(7)))
-    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV)
-    xbuf2 = torch.zeros_like(xbuf)
-    qx = torch.zeros(B * N, dtype=torch.int32, device=DEV)
+    xbufs = [torch.zeros(call("q3_attn_xbuf_words", B, Hq, splits), dtype=torch.int32, device=DEV) for _ in range(3)]
+    qxs = [torch.zeros(B * N, dtype=torch.int32, device=DEV) for _ in range(2)]
+    ox = torch.zeros(B * KO, dtype=torch.int32, device=DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    xm = _lib.X_EMBED_NORM if embed else _lib.X_NORM
     for layer, seed in ((0, 11), (1, 12), (0, 13)):
-        if layer == 0 and seed == 13:
-            xbuf.zero_()  # the same (position, layer) as the first round
-            xbuf2.zero_()
-            qx.zero_()
-        x = dv(rnd((B, K), 1.5, seed))
+        if layer == 0 and seed == 13:  # the same (position, layer) as the first round
+            for t in xbufs + qxs + [ox]:
+                t.zero_()
+        x = rnd((B, K), 1.5, seed)
         g = dv((1 + rnd((K,), 0.2, seed + 50).float()).to(torch.bfloat16))
         w = dv(rnd((N, K), 0.05, seed + 100))
-        xm = _lib.X_EMBED_NORM if embed else _lib.X_NORM
-        src = table if embed else x
-        outs, caches, resids = [], [], []
-        for fused in (False, True):
+        wo = dv(rnd((K, KO), 0.05, seed + 200))
+        runs = []
+        for mode in ("separate", "fused", "fused_o") if with_o else ("separate", "fused"):
             ckd, cvd = dv(ck), dv(cv)
-            out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
-            resid = torch.zeros(B, K, dtype=torch.bfloat16, device=DEV)
-            if fused:
-                call("q3_qkv_attn", xm, P(src), K, P(ids) if embed else None, P(g), 1e-6,
-                     P(resid) if embed else None, P(w), K, P(qx), P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd),
-                     P(cvd), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
-            else:
+            out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+            # The residual stream: the norm prologue's input, joined in place by o.
+            resid = dv(x) if not embed else torch.zeros(B, K, dtype=torch.bfloat16, device=DEV)
+            src = table if embed else resid
+            if mode == "separate":
                 qkv = torch.empty(B, N, dtype=torch.bfloat16, device=DEV)
                 gemv(xm, src, K, w, B, N, K, _lib.EPI_STORE, qkv, N, ids=ids if embed else None, norm_w=g,
                      resid_out=resid if embed else None)
                 call("q3_attn_decode_fused", P(qkv), N, None, 0, P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd),
-                     P(cvd), P(xbuf2), P(out), B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5, P(err), S())
+                     P(cvd), P(xbufs[0]), P(out), B, Hq, Hkv, C, splits, layer, 1e-6, D ** -0.5, P(err), S())
+                if with_o:
+                    gemv(_lib.X_PLAIN, out, KO, wo, B, K, KO, _lib.EPI_RESID, resid, K)
+            else:
+                o = mode == "fused_o"
+                call("q3_qkv_attn", xm, P(src), K, P(ids) if embed else None, P(g), 1e-6,
+                     P(resid) if embed or o else None, P(w), K, P(qxs[o]), P(qw), P(kw), P(cos), P(sin), P(posd),
+                     P(ckd), P(cvd), P(xbufs[1 + o]), None if o else P(out), P(wo) if o else None,
+                     P(ox) if o else None, B, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
+                if not o and with_o:
+                    gemv(_lib.X_PLAIN, out, KO, wo, B, K, KO, _lib.EPI_RESID, resid, K)
             torch.cuda.synchronize()
-            outs.append(out.cpu())
-            caches.append((ckd.cpu(), cvd.cpu()))
-            resids.append(resid.cpu())
-        assert torch.equal(outs[0], outs[1]), (layer, seed)
-        assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
-        assert torch.equal(resids[0], resids[1])
-        # Every projected row reached the exchange words with this step's flag.
+            runs.append((mode, out.cpu(), ckd.cpu(), cvd.cpu(), resid.cpu()))
+        ref = runs[0]
+        for mode, out, k_, v_, r_ in runs[1:]:
+            if mode != "fused_o":
+                assert torch.equal(out, ref[1]), (mode, layer, seed)
+            assert torch.equal(k_, ref[2]) and torch.equal(v_, ref[3]), (mode, layer, seed)
+            assert torch.equal(r_, ref[4]), (mode, layer, seed)
+        # Every projected row and attention output reached the exchange words with this step's flag.
         flag = 1 + (pos * 64 + layer) % 65535
-        words = qx.cpu().view(torch.int32).numpy().view(np.uint32)
-        assert (words >> 16 == flag).all()
+        for t in [qxs[0]] + ([qxs[1], ox] if with_o else []):
+            assert (t.cpu().numpy().view(np.uint32) >> 16 == flag).all()
     assert err.item() == 0
 
 
 def test_qkv_attn_refuses_what_it_is_not_built_for():
-    """Three rows, other widths and layers past the flag's field are refused
-    before anything is enqueued."""
-    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 2560) > 0
-    assert call("q3_qkv_attn_grid", 3, 32, 8, 1536, 6, 2560) == 0
-    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 4096) == 0
-    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 1, 2560) == 0   # one split: no fused attention
+    """Three rows, other widths, the o projection at two rows and layers past
+    the flag's field are refused before anything is enqueued."""
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 2560, 0) > 0
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 2560, 1) > 0
+    assert call("q3_qkv_attn_grid", 2, 32, 8, 700, 4, 2560, 1) == 0
+    assert call("q3_qkv_attn_grid", 3, 32, 8, 1536, 6, 2560, 0) == 0
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 16, 4096, 0) == 0
+    assert call("q3_qkv_attn_grid", 1, 32, 8, 1536, 1, 2560, 0) == 0   # one split: no fused attention
     Hq, Hkv, D, B, C, splits, K = 32, 8, 128, 1, 1536, 16, 2560
     N = (Hq + 2 * Hkv) * D
     x = torch.zeros(B, K, dtype=torch.bfloat16, device=DEV)
@@ -942,7 +956,13 @@ def test_qkv_attn_refuses_what_it_is_not_built_for():
     for layer, xm in ((64, _lib.X_NORM), (-1, _lib.X_NORM), (3, _lib.X_PLAIN)):
         with pytest.raises(RuntimeError):
             call("q3_qkv_attn", xm, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain), P(cos),
-                 P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), B, Hq, Hkv, C, splits, layer, D ** -0.5, None, S())
+                 P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), None, None, B, Hq, Hkv, C, splits, layer,
+                 D ** -0.5, None, S())
+    # The o projection without its exchange words or residual.
+    with pytest.raises(RuntimeError):
+        call("q3_qkv_attn", _lib.X_NORM, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain),
+             P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), None, P(w), None, B, Hq, Hkv, C, splits, 3,
+             D ** -0.5, None, S())
     torch.cuda.synchronize()
     assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and int(qx.abs().sum()) == 0
 
