@@ -254,7 +254,13 @@ int q3_attn_xbuf_words(int B, int Hq, int splits);
  * (X_PLAIN, EPI_RESID); the attention output goes to it as flagged words o_x
  * [Hq * 128] uint32 (16-byte aligned) and out may be NULL.  In X_EMBED_NORM
  * mode the join starts from the embedding row (resid_out is then written once,
- * by the join).
+ * by the join).  With next_w != NULL (and w_o), the workgroups that wait for
+ * the attention bring the first 1 KB of each row of the next launch's weights
+ * next_w [next_rows, K] into the L2 of the XCD that will read them -- the
+ * launch whose workgroup j reads rows next_group j .. next_group j +
+ * next_group - 1 and runs on XCD j % 8 (q3_gemv's gate/up projection at one
+ * row: next_group = next_rows / q3_gemv_partials(1, next_rows, Q3_EPI_SWIGLU))
+ * -- a cache hint with no effect on results (next_w may be NULL).
  * The caller zeroes qkv_x, xbuf and o_x before positions can repeat (a new
  * prompt); eps is both norms' epsilon.  Applies when q3_qkv_attn_grid(B, Hq,
  * Hkv, capacity, splits, K, w_o != NULL) > 0 (what q3_attn_fused_grid admits,
@@ -267,8 +273,9 @@ int q3_qkv_attn(int x_mode, const uint16_t *x, int ldx, const int64_t *ids, cons
                 float eps, uint16_t *resid_out, const uint16_t *w, int K, uint32_t *qkv_x,
                 const uint16_t *q_norm_w, const uint16_t *k_norm_w, const uint16_t *cos_table,
                 const uint16_t *sin_table, const int64_t *pos, uint16_t *cache_k, uint16_t *cache_v,
-                uint32_t *xbuf, uint16_t *out, const uint16_t *w_o, uint32_t *o_x, int B, int Hq, int Hkv,
-                int capacity, int splits, int layer, float scale, int *err, hipStream_t stream);
+                uint32_t *xbuf, uint16_t *out, const uint16_t *w_o, uint32_t *o_x, const uint16_t *next_w,
+                int next_rows, int next_group, int B, int Hq, int Hkv, int capacity, int splits, int layer,
+                float scale, int *err, hipStream_t stream);
 int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K, int with_o);
 
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1

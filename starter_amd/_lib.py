@@ -58,7 +58,7 @@ SIGNATURES = {
                              _P, _P],
     "q3_attn_fused_grid": [_I, _I, _I, _I, _I],
     "q3_attn_xbuf_words": [_I, _I, _I],
-    "q3_qkv_attn": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+    "q3_qkv_attn": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                     _I, _I, _I, _I, _I, _I, _F, _P, _P],
     "q3_qkv_attn_grid": [_I, _I, _I, _I, _I, _I, _I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],

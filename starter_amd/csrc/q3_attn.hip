@@ -726,7 +726,17 @@ struct OprojArgs {
     const bf16_t* table;   // X_EMBED_NORM launches: the embedding table, whose row ids[0] is the
     const int64_t* ids;    //   residual the join starts from (nothing else writes resid in this launch)
     const uint32_t* ox;    // the merged attention output as flagged words [K]
+    // The next launch's weights [nrows, N] (the gate/up projection), read by
+    // its workgroup j as rows ngroup j .. ngroup j + ngroup - 1 on XCD j % 8
+    // (a launch's workgroup i runs on XCD i % 8): the o workgroups past the
+    // merging ones bring the first WARM_BYTES of each such row into their
+    // XCD's L2 while they wait (null: no warming).  sink is never set (the
+    // loads' values must have a use).
+    const bf16_t* nw;
+    int nrows, ngroup;
+    uint32_t* sink;
 };
+constexpr int WARM_BYTES = 1024;
 // o rows per wave: QO_RN on the workgroups that are neither attention units
 // nor merging ones (idle once their q|k|v rows are stored, so their o weights
 // stream while the attention runs), QO_RA on attention workgroups for the rows
@@ -746,13 +756,43 @@ __device__ __forceinline__ void o_issue(const OprojArgs& o, int row0, u32x4_t (&
                 o.w + (int64_t)min(row0 + r, o.N - 1) * (512 * KUO) + lane * 8 + u * 512));
 }
 
+// The L2 warming of the next launch's rows: this workgroup is warming
+// workgroup `slot` of the `slots` on its XCD (x = blockIdx.x % 8), and takes
+// next workgroups j = x + 8 t for t = slot, slot + slots, ...  Loads are
+// plain (they allocate in L2) and unconditional (indices clamped).
+__device__ __forceinline__ void warm_next(const OprojArgs& o, int slot, int slots) {
+    const int x = blockIdx.x & 7, tid = threadIdx.x;
+    const int groups = o.nrows / o.ngroup;
+    const int per_x = (groups - x + 7) / 8;                // next workgroups on XCD x
+    const int mine = (per_x - slot + slots - 1) / slots;   // of which this workgroup warms
+    constexpr int LINES = WARM_BYTES / 128;
+    const int per_group = o.ngroup * LINES;
+    const int items = mine * per_group;
+    uint32_t acc = 0;
+    for (int e0 = 0; e0 < items; e0 += 256 * 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = min(e0 + u * 256 + tid, items - 1);
+            const int i = e / per_group, rem = e % per_group;
+            const int j = x + 8 * (slot + slots * i);
+            const int64_t row = (int64_t)j * o.ngroup + rem / LINES;
+            v[u] = *reinterpret_cast<const uint32_t*>(o.nw + row * o.N + (rem % LINES) * 64);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    if (o.sink != nullptr) o.sink[tid] = acc;
+}
+
 // Wait for the merged output (a few words first, one per merging workgroup,
 // then every word until all carry flag F), stage it in LDS, finish this
 // wave's rows.  Every wave of the workgroup calls it.  Bounded (1 s, then
-// *err and the payloads as they are).
-template <int XMODE, int R, int KUO>
+// *err and the payloads as they are).  first() runs once, after the first
+// round of polls (which waited for this wave's o weights).
+template <int XMODE, int R, int KUO, class First = NoMid>
 __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32x4_t (&wo)[R][KUO], uint32_t F,
-                                         int* err, bf16_t* xo) {
+                                         int* err, bf16_t* xo, First first = First()) {
     constexpr int K = 512 * KUO;
     constexpr int WPT = K / 256;  // words per thread
     static_assert(WPT % 4 == 0, "whole 16-byte loads");
@@ -762,10 +802,12 @@ __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32
     q3x::SpinBound sb;
     bool ok = true;
     // One word per 256 (a merging workgroup's share) until those are current.
-    for (;;) {
+    for (bool once = true;; once = false) {
         const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (min(lane, K / 256 - 1) * 256 + 255), 0,
                                                                 q3x::SC1);
-        if (__all(((v ^ Fs) & 0xffff0000u) == 0)) break;
+        const bool done = __all(((v ^ Fs) & 0xffff0000u) == 0);
+        if (once) first();
+        if (done) break;
         __builtin_amdgcn_s_sleep(2);
         if (!sb.ok(q3x::SPIN_LIMIT)) {
             ok = false;
@@ -862,7 +904,13 @@ __global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeA
             const int row0 = (j * 4 + wave) * QO_RN;
             u32x4_t wo[QO_RN][KUO];
             o_issue<QO_RN, KUO>(o, row0, wo);
-            o_finish<XMODE, QO_RN, KUO>(o, row0, wo, F, a.err, xs);
+            // Warming workgroups: these n_on, slot = rank among those on this XCD.
+            const int f = n_att + n_mrg, fx = f + ((bid - f) & 7);
+            const int slot = (bid - fx) >> 3, slots = (f + n_on - fx + 7) >> 3;
+            const auto warm = [&]() {
+                if (o.nw != nullptr) warm_next(o, slot, slots);
+            };
+            o_finish<XMODE, QO_RN, KUO>(o, row0, wo, F, a.err, xs, warm);
         }
     }
 }
@@ -1398,8 +1446,9 @@ extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* 
                            float eps, bf16_t* resid_out, const bf16_t* w, int K, uint32_t* qkv_x,
                            const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
                            const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
-                           uint32_t* xbuf, bf16_t* out, const bf16_t* w_o, uint32_t* o_x, int B, int Hq, int Hkv,
-                           int capacity, int splits, int layer, float scale, int* err, hipStream_t stream) {
+                           uint32_t* xbuf, bf16_t* out, const bf16_t* w_o, uint32_t* o_x, const bf16_t* next_w,
+                           int next_rows, int next_group, int B, int Hq, int Hkv, int capacity, int splits, int layer,
+                           float scale, int* err, hipStream_t stream) {
     const bool with_o = w_o != nullptr;
     const int grid = q3_qkv_attn_grid(B, Hq, Hkv, capacity, splits, K, with_o ? 1 : 0);
     const bool emb = x_mode == Q3_X_EMBED_NORM;
@@ -1409,6 +1458,8 @@ extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* 
         (with_o ? (!o_x || !resid_out || (reinterpret_cast<uintptr_t>(w_o) & 15) ||
                    (reinterpret_cast<uintptr_t>(o_x) & 15))
                 : !out) ||
+        (next_w && (!with_o || next_group < 1 || next_rows < next_group || (next_rows % next_group) != 0 ||
+                    (reinterpret_cast<uintptr_t>(next_w) & 3) || K * 2 < WARM_BYTES)) ||
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(norm_w) |
           reinterpret_cast<uintptr_t>(xbuf)) & 15) ||
         (reinterpret_cast<uintptr_t>(qkv_x) & 3) || (emb && (reinterpret_cast<uintptr_t>(resid_out) & 15)))
@@ -1419,7 +1470,8 @@ extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* 
     const QkvGemvArgs g{x, ldx, ids, norm_w, eps, with_o ? nullptr : resid_out, w, N, qkv_x};
     DecodeArgs a{nullptr, N, nullptr, 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
                  nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B, qkv_x, err, with_o ? o_x : nullptr};
-    const OprojArgs o{w_o, K, with_o ? resid_out : nullptr, emb ? x : nullptr, ids, o_x};
+    const OprojArgs o{w_o, K, with_o ? resid_out : nullptr, emb ? x : nullptr, ids, o_x, next_w, next_rows,
+                      next_group, nullptr};
     const QaPlan p = qa_plan(B, Hq, Hkv, splits, K, with_o);
     const void* fn = qkv_attn_kernel_for(B, K, x_mode, p.ra, with_o ? qkv_attn_kuo(B, Hq, K) : 0);
     int n_gemv = p.n_gemv, n_on = p.n_on, n_oa = p.n_oa;

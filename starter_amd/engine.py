@@ -300,6 +300,9 @@ class Engine:
                            call("q3_qkv_attn_grid", B, self.HEADS, Hkv, capacity, self.splits, H, 1) > 0)
         self.qkv_x = torch.zeros(B * self.qkv_size if self.qkv_attn else 4, dtype=torch.int32, device=self.device)
         self.o_x = torch.zeros(B * self.q_size if self.qkv_attn_o else 4, dtype=torch.int32, device=self.device)
+        # Rows per workgroup of the gate/up GEMV, whose weights that launch
+        # brings into L2 ahead of it.
+        self.gate_up_group = 2 * self.INTER // call("q3_gemv_partials", B, 2 * self.INTER, _lib.EPI_SWIGLU)
         self.skinny = not self.small and B <= SKINNY_BATCH_MAX and self._skinny_shapes_ok(B)
         # Split-K workspace of the MFMA decode projections: every projection's
         # partials, [splits, B, N] FP32, one consumer at a time.
@@ -393,6 +396,7 @@ class Engine:
                      _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
                      vc0 + i * layer_stride, _ptr(self.attn_x), None if with_o else attn,
                      _ptr(L["o"]) if with_o else None, _ptr(self.o_x) if with_o else None,
+                     _ptr(L["gate_up"]) if with_o else None, 2 * I, self.gate_up_group,
                      B, Hq, Hkv, C, self.splits, i, self.SCALE, _ptr(self.attn_err), s)
             elif self.small:
                 if i == 0:

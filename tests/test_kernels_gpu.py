@@ -910,10 +910,12 @@ def test_qkv_attn_matches_projection_then_fused_attention(B, Hkv, K, C, pos, spl
                     gemv(_lib.X_PLAIN, out, KO, wo, B, K, KO, _lib.EPI_RESID, resid, K)
             else:
                 o = mode == "fused_o"
+                # With o, also the L2 hint for a following gate/up GEMV (no effect on results).
                 call("q3_qkv_attn", xm, P(src), K, P(ids) if embed else None, P(g), 1e-6,
                      P(resid) if embed or o else None, P(w), K, P(qxs[o]), P(qw), P(kw), P(cos), P(sin), P(posd),
                      P(ckd), P(cvd), P(xbufs[1 + o]), None if o else P(out), P(wo) if o else None,
-                     P(ox) if o else None, B, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
+                     P(ox) if o else None, P(w) if o else None, N, 16, B, Hq, Hkv, C, splits, layer, D ** -0.5,
+                     P(err), S())
                 if not o and with_o:
                     gemv(_lib.X_PLAIN, out, KO, wo, B, K, KO, _lib.EPI_RESID, resid, K)
             torch.cuda.synchronize()
@@ -956,13 +958,23 @@ def test_qkv_attn_refuses_what_it_is_not_built_for():
     for layer, xm in ((64, _lib.X_NORM), (-1, _lib.X_NORM), (3, _lib.X_PLAIN)):
         with pytest.raises(RuntimeError):
             call("q3_qkv_attn", xm, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain), P(cos),
-                 P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), None, None, B, Hq, Hkv, C, splits, layer,
-                 D ** -0.5, None, S())
-    # The o projection without its exchange words or residual.
+                 P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), None, None, None, 0, 0, B, Hq, Hkv, C, splits,
+                 layer, D ** -0.5, None, S())
+    # The o projection without its exchange words or residual; the L2 hint
+    # without the o projection, or with a row group that does not divide.
     with pytest.raises(RuntimeError):
         call("q3_qkv_attn", _lib.X_NORM, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain),
-             P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), None, P(w), None, B, Hq, Hkv, C, splits, 3,
-             D ** -0.5, None, S())
+             P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), None, P(w), None, None, 0, 0, B, Hq, Hkv, C, splits,
+             3, D ** -0.5, None, S())
+    with pytest.raises(RuntimeError):
+        call("q3_qkv_attn", _lib.X_NORM, P(x), K, None, P(gain), 1e-6, None, P(w), K, P(qx), P(gain), P(gain),
+             P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), P(out), None, None, P(w), N, 16, B, Hq, Hkv, C,
+             splits, 3, D ** -0.5, None, S())
+    ox = torch.zeros(Hq * D, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError):
+        call("q3_qkv_attn", _lib.X_NORM, P(x), K, None, P(gain), 1e-6, P(x), P(w), K, P(qx), P(gain), P(gain),
+             P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), None, P(w), P(ox), P(w), N, 7, B, Hq, Hkv, C,
+             splits, 3, D ** -0.5, None, S())
     torch.cuda.synchronize()
     assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and int(qx.abs().sum()) == 0
 
