@@ -239,6 +239,21 @@ int q3_attn_decode_fused(const uint16_t *qkv, int ld_qkv, const float *qkv_part,
                          float eps, float scale, int *err, hipStream_t stream);
 int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int splits);
 int q3_attn_xbuf_words(int B, int Hq, int splits);
+/* q3_attn_decode with two splits + q3_attn_merge in one launch, where
+ * q3_attn_splits keeps one split for 65-128 (sequence, KV head) pairs (B=16 at
+ * up to 4096 keys): one eight-wave workgroup per split on every CU; split 1
+ * leaves its partial as flagged words in xbuf [q3_attn_xbuf_words(B, Hq, 2)]
+ * and split 0 folds it into its own as the merge does.  Same bits as the two
+ * launches; xbuf, layer and err as for q3_attn_decode_fused.  Applies when
+ * q3_attn_pair_grid(B, Hq, Hkv, capacity) > 0.  Replaces fused.py:641-846
+ * (decode_attention_gqa, or split + merge) with one launch. */
+int q3_attn_decode_pair(const uint16_t *qkv, int ld_qkv, const float *qkv_part, int qkv_splits,
+                        const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                        const uint16_t *cos_table, const uint16_t *sin_table, const int64_t *pos,
+                        uint16_t *cache_k, uint16_t *cache_v, uint32_t *xbuf, uint16_t *out,
+                        int B, int Hq, int Hkv, int capacity, int layer, float eps, float scale, int *err,
+                        hipStream_t stream);
+int q3_attn_pair_grid(int B, int Hq, int Hkv, int capacity);
 
 /* The q|k|v projection (q3_gemv with x_mode X_NORM or X_EMBED_NORM and
  * EPI_STORE: x, ldx, ids, norm_w, eps, resid_out and w [N, K] as there, N =

@@ -246,9 +246,14 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // mid() runs once every load of the prologue is in flight and before any wait
 // for one (every wave of the workgroup calls it): the fused q|k|v projection
 // computes its rows there while this unit's first key block streams in.
+//
+// With `partner` (split 0 of a two-split pair): split 1 of the same launch
+// leaves its record there as flagged words; this unit folds it into its own
+// partial exactly as attn_merge_kernel folds two splits and writes the
+// normalised output (the wait is bounded: 1 s, then *a.err).
 template <int WAVES, int QP, class Mid = NoMid>
 __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kvh, int b, uint32_t* xbuf, uint32_t F,
-                                          Mid mid = Mid()) {
+                                          Mid mid = Mid(), const uint32_t* partner = nullptr) {
     static_assert(WAVES == 4 || WAVES == 8, "four or eight waves");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -295,6 +300,15 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
     const int end = bad_pos ? begin : min(range_end, pos + 1);
     const bool owner = !bad_pos && begin <= pos && pos < end;
     const Pair16 cr = pair16(a.cos_t + (int64_t)pos * D, lane), sr = pair16(a.sin_t + (int64_t)pos * D, lane);
+    // The second key block too, behind those small loads: waiting for them
+    // then waits for the first block only, and the CU streams both blocks
+    // without a gap.  A wave with one block or none reads one row of its range
+    // over and over instead (cache hits), so the load stays unconditional.
+    // With q|k|v from the same launch (mid() holds the projection's weights)
+    // the second block is requested after the wait for q|k|v instead.
+    const int stride = contig ? BLK : WAVES * BLK;
+    const int wend = contig ? min(first + wq, end) : end;
+    const int nblk = first < end ? (wend - first + stride - 1) / stride : 0;
     __builtin_amdgcn_sched_barrier(0);
     mid();
     if constexpr (QP == 3) qkv_poll(a, b, qidx, kidx, vidx, F, qr, kr, vr);
@@ -353,11 +367,10 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * kk + 8 * g]);
             st.qb[kk] = as_bf16x8(v);
         }
-        const int stride = contig ? BLK : WAVES * BLK;
-        const int wend = contig ? min(first + wq, end) : end;
-        const int nblk = (wend - first + stride - 1) / stride;
         auto sub = [&](int blk) { return (owner && blk <= pos && pos < blk + BLK) ? pos - blk : -1; };
-        // Every load inside the loop is unconditional and the last one or two
+        // At the top of the loop ra holds block it and rb block it + 1, both
+        // requested.  Every load inside the loop is unconditional (past the
+        // last block, rows clamp to the last row) and the last one or two
         // blocks are peeled: the compiler's wait counting, which merges
         // control-flow paths conservatively, then waits for exactly the set
         // about to be used and leaves the other in flight.
@@ -397,6 +410,20 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
     // skipped by selects; the fold's operations and order are unchanged.
     constexpr int EPT = GROUP * D / (WAVES * 64);
     static_assert(EPT * WAVES * 64 == GROUP * D, "whole elements per thread");
+    // The partner's record, requested before the fold (it usually finished
+    // first: its range holds the later, partly empty keys).
+    u32x2_t pw[EPT];
+    u32x4_t pm[EPT];
+    const auto prs = q3x::rsrc(partner != nullptr ? partner : xbuf);
+    const auto precord = [&](int i) {
+        const int e = tid + i * WAVES * 64, h = e / D, d = e % D;
+        const int off = (int)(((int64_t)b * a.Hq + kvh * GROUP + h) * a.splits + 1) * XREC * 4;
+        pw[i] = __builtin_amdgcn_raw_buffer_load_b64(prs, off + 8 * d, 0, q3x::SC1);
+        pm[i] = q3x::ld_coh(prs, off + 4 * 2 * D);
+    };
+    if (partner != nullptr)
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) precord(i);
     float wm[EPT][WAVES], wl[EPT][WAVES], wa[EPT][WAVES];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
@@ -423,6 +450,46 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
         }
         const int qh = kvh * GROUP + h;
         const int64_t p = ((int64_t)b * a.Hq + qh) * a.splits + split;
+        if (partner != nullptr) {
+            const uint32_t Fs = F << 16;
+            q3x::SpinBound sb;
+            for (;;) {
+                const uint32_t bad = (((pw[i].x ^ Fs) | (pw[i].y ^ Fs)) & 0xffff0000u) | q3x::unflagged(pm[i], Fs);
+                if (__all(bad == 0)) break;
+                __builtin_amdgcn_s_sleep(1);
+                if (!sb.ok(q3x::SPIN_LIMIT)) {
+                    if (a.err != nullptr && lane == 0)
+                        __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                precord(i);
+            }
+            // attn_merge_kernel's fold of splits 0 (this unit) and 1.
+            const float av[2] = {sacc, q3x::funpack(pw[i].x, pw[i].y)};
+            const float mv[2] = {M, q3x::funpack(pm[i].x, pm[i].y)};
+            const float lv[2] = {sl, q3x::funpack(pm[i].z, pm[i].w)};
+            float m_run = -INFINITY, l_run = 0.f, acc = 0.f, cm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (lv[j] > 0.f) cm = fmaxf(cm, mv[j]);
+            if (cm != -INFINITY) {
+                const float m_new = fmaxf(m_run, cm);
+                const float scale = expf(m_run - m_new);
+                acc *= scale;
+                l_run *= scale;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float ls = lv[j];
+                    if (ls > 0.f) {
+                        const float wt = expf(mv[j] - m_new);
+                        acc += av[j] * wt;
+                        l_run += ls * wt;
+                    }
+                }
+            }
+            a.out[((int64_t)b * a.Hq + qh) * D + d] = (bf16_t)f2bf(l_run > 0.f ? acc / l_run : 0.f);
+            continue;
+        }
         if (xbuf != nullptr) {  // flagged record for the merging workgroups of the same launch
             const auto rs = q3x::rsrc(xbuf);
             const int off = (int)p * XREC * 4;
@@ -915,6 +982,22 @@ __global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeA
     }
 }
 
+// Two splits, eight waves, one workgroup per CU, no merge launch: workgroup
+// 2 u + 1 is split 1 of (sequence, KV head) u and leaves its record as
+// flagged words in xbuf; workgroup 2 u is split 0 and folds that record into
+// its own (attn_unit's partner mode).  For 128 (sequence, KV head) pairs,
+// whose single split would leave half the CUs idle.  The whole grid is
+// resident at once (the launcher checks).  Same bits as q3_attn_decode with
+// two splits and q3_attn_merge.
+template <int QP>
+__global__ __launch_bounds__(512, 1) void attn_pair_kernel(DecodeArgs a, uint32_t* xbuf, int layer) {
+    const uint32_t F = step_flag((int)*a.pos, layer);
+    const int u = blockIdx.x >> 1, split = blockIdx.x & 1;
+    const int kvh = u % a.Hkv, b = u / a.Hkv;
+    if (split == 1) attn_unit<8, QP>(a, 1, kvh, b, xbuf, F);
+    else attn_unit<8, QP>(a, 0, kvh, b, nullptr, F, NoMid(), xbuf);
+}
+
 // grid (Hq, B), 128 threads (one per d): log-sum-exp merge of the split
 // partials (reference fused.py:793-823).  Latency-shaped: the (max, sum)
 // pairs go through LDS in one cooperative load, the accumulators are read 16
@@ -1310,6 +1393,61 @@ extern "C" int q3_attn_fused_grid(int B, int Hq, int Hkv, int capacity, int spli
 }
 
 extern "C" int q3_attn_xbuf_words(int B, int Hq, int splits) { return B * Hq * splits * XREC; }
+
+// Workgroups of the pair kernel resident at once on the current device (0 if
+// unknown), cached per device.
+static int pair_resident() {
+    constexpr int MAX_DEV = 64;
+    static int cached[MAX_DEV];  // 0 = not yet asked; -1 = unknown
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    if (cached[dev] != 0) return cached[dev] > 0 ? cached[dev] : 0;
+    int cus = 0, per = 1 << 30;
+    bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
+    for (const void* f : {reinterpret_cast<const void*>(attn_pair_kernel<0>),
+                          reinterpret_cast<const void*>(attn_pair_kernel<1>),
+                          reinterpret_cast<const void*>(attn_pair_kernel<2>)}) {
+        int n = 0;
+        ok = ok && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 512, 0) == hipSuccess;
+        per = n < per ? n : per;
+    }
+    ok = ok && per >= 1;
+    cached[dev] = ok ? per * cus : -1;
+    return ok ? per * cus : 0;
+}
+
+// Grid of the pair kernel, or 0 where it does not apply: where q3_attn_splits
+// keeps one split at 65-128 (sequence, KV head) pairs (at least 256 keys per
+// half, so every wave of both units gets keys), with the grid resident.  At
+// B=16 and 768 keys the single split runs eight-wave workgroups on half the
+// CUs; two splits with a merge launch measured no faster.
+extern "C" int q3_attn_pair_grid(int B, int Hq, int Hkv, int capacity) {
+    if (B < 1 || Hkv < 1 || Hq != GROUP * Hkv || capacity < 1) return 0;
+    const long heads = (long)B * Hkv;
+    if (heads > 128 || heads <= 64 || q3_attn_splits(B, Hkv, capacity) != 1 || split_len(capacity, 2) < 8 * BLK)
+        return 0;
+    const long grid = 2 * heads;
+    return grid <= pair_resident() ? (int)grid : 0;
+}
+
+extern "C" int q3_attn_decode_pair(const bf16_t* qkv, int ld_qkv, const float* qkv_part, int qkv_splits,
+                                   const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
+                                   const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
+                                   uint32_t* xbuf, bf16_t* out, int B, int Hq, int Hkv, int capacity, int layer,
+                                   float eps, float scale, int* err, hipStream_t stream) {
+    const int grid = q3_attn_pair_grid(B, Hq, Hkv, capacity);
+    if (grid == 0 || layer < 0 || layer >= 64 || ld_qkv < (Hq + 2 * Hkv) * D || (!qkv && !qkv_part) ||
+        (qkv_part && (qkv_splits < 1 || (reinterpret_cast<uintptr_t>(qkv_part) & 3))) || !pos || !cache_k ||
+        !cache_v || !xbuf || !out || (reinterpret_cast<uintptr_t>(xbuf) & 15))
+        return (int)hipErrorInvalidValue;
+    DecodeArgs a{qkv, ld_qkv, qkv_part, qkv_part ? qkv_splits : 0, q_norm_w, k_norm_w, cos_table, sin_table, pos,
+                 cache_k, cache_v, nullptr, nullptr, out, Hq, Hkv, capacity, 2, eps, scale, B, nullptr, err};
+    const int qp = !qkv_part ? 0 : qkv_splits <= QKV_FAST ? 1 : 2;
+    if (qp == 0) Q3_LAUNCH((attn_pair_kernel<0>), dim3(grid), dim3(512), 0, stream, a, xbuf, layer);
+    else if (qp == 1) Q3_LAUNCH((attn_pair_kernel<1>), dim3(grid), dim3(512), 0, stream, a, xbuf, layer);
+    else Q3_LAUNCH((attn_pair_kernel<2>), dim3(grid), dim3(512), 0, stream, a, xbuf, layer);
+    Q3_CHECK_LAUNCH();
+}
 
 static int attn_fused_launch(const bf16_t* qkv, int ld_qkv, const float* qkv_part, int qkv_splits,
                              const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,

@@ -285,10 +285,20 @@ class Engine:
         # at the start of every call, and a timeout word checked every step.
         # The exchange words' flag encodes (position, layer) with layer < 64
         # (q3_attn_decode_fused), so deeper models keep the two launches.
-        self.attn_fused = (FUSED_ATTENTION and self.splits > 1 and
-                           self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and
-                           call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity, self.splits) > 0)
-        words = call("q3_attn_xbuf_words", B, self.HEADS, self.splits) if self.attn_fused else 4
+        # Where one split would leave half the CUs idle (128 sequence x KV head
+        # pairs), two splits whose second hands its partial to the first; the
+        # two-launch path then also takes two splits (and a merge launch), so
+        # both compute the same bits.
+        if self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and call("q3_attn_pair_grid", B, self.HEADS, Hkv, capacity):
+            self.splits = 2
+        self.attn_pair = FUSED_ATTENTION and self.splits == 2 and call("q3_attn_pair_grid", B, self.HEADS, Hkv,
+                                                                        capacity) > 0
+        self.attn_fused = self.attn_pair or (FUSED_ATTENTION and self.splits > 1 and
+                                             self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and
+                                             call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity,
+                                                  self.splits) > 0)
+        words = (call("q3_attn_xbuf_words", B, self.HEADS, 2 if self.attn_pair else self.splits)
+                 if self.attn_fused else 4)
         self.attn_x = torch.zeros(words, dtype=torch.int32, device=self.device)
         self.attn_err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.small = B <= GEMV_BATCH_MAX
@@ -478,11 +488,16 @@ class Engine:
 
     def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int) -> None:
         """Layer i's decode attention into attn_out: q/k norm + RoPE + KV append,
-        split-K GQA and the split merge (one launch when ``attn_fused``).
+        split-K GQA and the split merge (one launch when ``attn_fused``: merging
+        workgroups, or two splits of which the first merges, ``attn_pair``).
         ``src`` is (qkv, ld, qkv partials, partial count)."""
         B, Hq, Hkv, C, s = self.batch, self.HEADS, self.KV_HEADS, self.capacity, self._s
         pos, attn = _ptr(self.g_pos), _ptr(self.attn_out)
         common = (_ptr(L["q_norm"]), _ptr(L["k_norm"]), _ptr(self.cos_table), _ptr(self.sin_table), pos, kc, vc)
+        if self.attn_pair:
+            call("q3_attn_decode_pair", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, i, self.EPS,
+                 self.SCALE, _ptr(self.attn_err), s)
+            return
         if self.attn_fused:
             call("q3_attn_decode_fused", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i,
                  self.EPS, self.SCALE, _ptr(self.attn_err), s)

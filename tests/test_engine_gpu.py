@@ -187,13 +187,15 @@ def _trace_attention(engine, ids, n, fused):
     return steps, logits, tokens
 
 
-@pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700), (4, 260), (5, 300)])
+@pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700), (4, 260), (5, 300), (64, 600)])
 def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, batch, prompt):
     """Contexts long enough for split attention (2..16 splits, grid resident at
     once) run attention and its split merge as one launch.  Same bits as the
     two-launch path at every step, for trace_logits and generate, across
     repeated calls (the exchange words are cleared per call), and the oracle's
-    stream.  Batch 5 takes the MFMA (tiled-weight) step."""
+    stream.  Batches 5 and 64 take the MFMA (tiled-weight) step; at 64 (128
+    sequence x KV head pairs, where the two-launch path keeps one split) the
+    launch is two splits whose second hands its partial to the first."""
     cfg, tensors = load_checkpoint(tile_ckpt)
     rng = np.random.Generator(np.random.PCG64(900 + batch))
     ids = rng.integers(0, cfg.vocab_size, (batch, prompt)).tolist()
@@ -203,7 +205,15 @@ def test_fused_attention_launch_matches_two_launches(tile_engine, tile_ckpt, bat
     assert f_steps == s_steps == f_tokens == s_tokens
     orc = oc.Qwen3Oracle(cfg, tensors, torch.bfloat16)
     want, want_logits = orc.generate(ids, 8, keep_logits=True)
-    check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), TOL_TINY)
+    # Bound: TOL_TINY, or twice the reordering floor of the first logits (the
+    # oracle with FP32-GEMM projections against itself) where it is larger --
+    # over 64 rows of 600 tokens the largest deviation is (0.062 measured).
+    orc.linear = oc.f32_linear()
+    orc.reset(batch, prompt + 8)
+    floor = float((orc.prefill(torch.tensor(ids)).float() - want_logits[0].float()).abs().max())
+    tol = max(TOL_TINY, 2.0 * floor)
+    print(f"reordering floor of the first logits {floor:.3f}; bound {tol:.3f}")
+    check_stream(f_steps, f_logits.float().numpy(), want, torch.stack(want_logits).float().numpy(), tol)
 
 
 @pytest.mark.parametrize("batch,prompt", [(1, 300), (2, 700)])

@@ -850,6 +850,70 @@ def test_attn_decode_fused_rejects_layers_past_its_flag():
     assert bool((out.float() == 7.0).all()) and int(ck.abs().sum()) == 0 and err.item() == 0
 
 
+@pytest.mark.parametrize("B,Hkv,C,pos,qsplits", [(16, 8, 768, 600, 0),    # config 3's shape
+                                                  (16, 8, 768, 383, 5),    # split 1 holds no key yet
+                                                  (16, 8, 768, 384, 0),    # its first key
+                                                  (16, 8, 1024, 1023, 5),
+                                                  (16, 8, 4096, 4000, 9),  # partials summed by the loop
+                                                  (64, 2, 600, 599, 3)])   # the tile test model at 64 rows
+def test_attn_decode_pair_matches_two_splits_and_merge(B, Hkv, C, pos, qsplits):
+    """Two splits in one launch, split 0 folding split 1's flagged record ==
+    q3_attn_decode with two splits then q3_attn_merge, bit for bit, output and
+    caches, over several layers' flags; a zeroed exchange buffer makes a
+    repeated (position, layer) safe."""
+    Hq, D = 4 * Hkv, 128
+    width = (Hq + 2 * Hkv) * D
+    assert call("q3_attn_splits", B, Hkv, C) == 1
+    assert call("q3_attn_pair_grid", B, Hq, Hkv, C) == 2 * B * Hkv
+    qw = (1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16)
+    kw = (1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16)
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    posd = dv(torch.tensor([pos]))
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", B, Hq, 2), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for layer, seed in ((0, 7), (1, 8), (0, 9)):
+        if layer == 0 and seed == 9:
+            xbuf.zero_()  # the same (position, layer) as the first round
+        if qsplits:
+            part = (torch.randn(qsplits, B, width, generator=torch.Generator().manual_seed(seed)) * 0.7).float()
+            src = (None, width, P(dv(part)), qsplits)
+        else:
+            src = (P(dv(rnd((B, width), 1.5, seed))), width, None, 0)
+        outs, caches = [], []
+        for pair in (False, True):
+            ckd, cvd = dv(ck), dv(cv)
+            out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=DEV)
+            if pair:
+                call("q3_attn_decode_pair", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd), P(ckd),
+                     P(cvd), P(xbuf), P(out), B, Hq, Hkv, C, layer, 1e-6, D ** -0.5, P(err), S())
+            else:
+                pacc = torch.empty(B, Hq, 2, D, dtype=torch.float32, device=DEV)
+                pml = torch.empty(B, Hq, 2, 2, dtype=torch.float32, device=DEV)
+                call("q3_attn_decode", *src, P(dv(qw)), P(dv(kw)), P(dv(cos)), P(dv(sin)), P(posd), P(ckd),
+                     P(cvd), P(pacc), P(pml), None, B, Hq, Hkv, C, 2, 1e-6, D ** -0.5, S())
+                call("q3_attn_merge", P(pacc), P(pml), P(out), B, Hq, 2, S())
+            torch.cuda.synchronize()
+            outs.append(out.cpu())
+            caches.append((ckd.cpu(), cvd.cpu()))
+        assert torch.equal(outs[0], outs[1]), (layer, seed)
+        assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    assert err.item() == 0
+
+
+def test_attn_pair_applies_where_one_split_leaves_cus_idle():
+    """The pair launch takes 65-128 (sequence, KV head) pairs where the split
+    policy keeps one split, with at least 256 keys per half."""
+    assert call("q3_attn_pair_grid", 16, 32, 8, 768) == 256
+    assert call("q3_attn_pair_grid", 16, 32, 8, 4096) == 256
+    assert call("q3_attn_pair_grid", 16, 32, 8, 4200) == 0   # more than 4096 keys: several splits
+    assert call("q3_attn_pair_grid", 16, 32, 8, 480) == 256  # 240 keys per half, ranges rounded to 256
+    assert call("q3_attn_pair_grid", 16, 32, 8, 448) == 0    # under 256 keys per half
+    assert call("q3_attn_pair_grid", 64, 32, 8, 2176) == 0   # 512 pairs fill the CUs with one split
+    assert call("q3_attn_pair_grid", 8, 32, 8, 16512) == 0
+    assert call("q3_attn_pair_grid", 1, 32, 8, 1536) == 0
+
+
 @pytest.mark.parametrize("B,Hkv,K,C,pos,splits,embed", [
     (1, 8, 2560, 1536, 1100, 16, False),   # config 2's shape: 16 splits of 96 keys
     (1, 8, 2560, 1536, 1535, 12, True),    # last slot, layer 0's embedding prologue
