@@ -300,15 +300,6 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
     const int end = bad_pos ? begin : min(range_end, pos + 1);
     const bool owner = !bad_pos && begin <= pos && pos < end;
     const Pair16 cr = pair16(a.cos_t + (int64_t)pos * D, lane), sr = pair16(a.sin_t + (int64_t)pos * D, lane);
-    // The second key block too, behind those small loads: waiting for them
-    // then waits for the first block only, and the CU streams both blocks
-    // without a gap.  A wave with one block or none reads one row of its range
-    // over and over instead (cache hits), so the load stays unconditional.
-    // With q|k|v from the same launch (mid() holds the projection's weights)
-    // the second block is requested after the wait for q|k|v instead.
-    const int stride = contig ? BLK : WAVES * BLK;
-    const int wend = contig ? min(first + wq, end) : end;
-    const int nblk = first < end ? (wend - first + stride - 1) / stride : 0;
     __builtin_amdgcn_sched_barrier(0);
     mid();
     if constexpr (QP == 3) qkv_poll(a, b, qidx, kidx, vidx, F, qr, kr, vr);
@@ -367,10 +358,11 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
             if (n < GROUP) v = *reinterpret_cast<const uint4*>(&qs[n][32 * kk + 8 * g]);
             st.qb[kk] = as_bf16x8(v);
         }
+        const int stride = contig ? BLK : WAVES * BLK;
+        const int wend = contig ? min(first + wq, end) : end;
+        const int nblk = (wend - first + stride - 1) / stride;
         auto sub = [&](int blk) { return (owner && blk <= pos && pos < blk + BLK) ? pos - blk : -1; };
-        // At the top of the loop ra holds block it and rb block it + 1, both
-        // requested.  Every load inside the loop is unconditional (past the
-        // last block, rows clamp to the last row) and the last one or two
+        // Every load inside the loop is unconditional and the last one or two
         // blocks are peeled: the compiler's wait counting, which merges
         // control-flow paths conservatively, then waits for exactly the set
         // about to be used and leaves the other in flight.
@@ -1320,6 +1312,10 @@ extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     if (heads * most < 128) {
         const long fine = (capacity + 95) / 96;
         most = fine <= 16 ? fine : (capacity + 127) / 128;
+        // One or two sequences: at least two splits where the cache holds two
+        // key blocks, so the attention can join the projections' launch
+        // (q3_qkv_attn needs the merging workgroups).
+        if (B <= 2 && capacity >= 2 * BLK && most < 2) most = 2;
     }
     const long s = want < most ? want : most;
     return s < 1 ? 1 : (int)s;

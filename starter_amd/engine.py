@@ -265,6 +265,15 @@ class Engine:
 
         B, H, V = batch, self.HIDDEN, self.VOCAB
         self.splits = call("q3_attn_splits", B, Hkv, capacity)
+        # Where one split would leave half the CUs idle (128 sequence x KV head
+        # pairs), two splits whose second hands its partial to the first; the
+        # two-launch path then also takes two splits (and a merge launch), so
+        # both compute the same bits.  Decided before anything is sized by the
+        # split count.
+        pair_ok = (self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and
+                   call("q3_attn_pair_grid", B, self.HEADS, Hkv, capacity) > 0)
+        if pair_ok:
+            self.splits = 2
         self.g_token = torch.zeros(B, dtype=torch.int64, device=self.device)
         self.g_pos = torch.zeros(1, dtype=torch.int64, device=self.device)
         self.g_counter = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -285,14 +294,7 @@ class Engine:
         # at the start of every call, and a timeout word checked every step.
         # The exchange words' flag encodes (position, layer) with layer < 64
         # (q3_attn_decode_fused), so deeper models keep the two launches.
-        # Where one split would leave half the CUs idle (128 sequence x KV head
-        # pairs), two splits whose second hands its partial to the first; the
-        # two-launch path then also takes two splits (and a merge launch), so
-        # both compute the same bits.
-        if self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and call("q3_attn_pair_grid", B, self.HEADS, Hkv, capacity):
-            self.splits = 2
-        self.attn_pair = FUSED_ATTENTION and self.splits == 2 and call("q3_attn_pair_grid", B, self.HEADS, Hkv,
-                                                                        capacity) > 0
+        self.attn_pair = FUSED_ATTENTION and pair_ok
         self.attn_fused = self.attn_pair or (FUSED_ATTENTION and self.splits > 1 and
                                              self.LAYERS <= FUSED_ATTENTION_MAX_LAYERS and
                                              call("q3_attn_fused_grid", B, self.HEADS, Hkv, capacity,
@@ -502,6 +504,10 @@ class Engine:
             call("q3_attn_decode_fused", *src, *common, _ptr(self.attn_x), attn, B, Hq, Hkv, C, self.splits, i,
                  self.EPS, self.SCALE, _ptr(self.attn_err), s)
             return
+        # The partial buffers hold [B, Hq, splits] records; the launcher cannot see their size.
+        records = B * Hq * self.splits
+        if self.part_acc.numel() < records * self.HEAD_DIM or self.part_ml.numel() < records * 2:
+            raise RuntimeError("attention partial buffers are smaller than the split count needs")
         call("q3_attn_decode", *src, *common, _ptr(self.part_acc), _ptr(self.part_ml),
              attn if self.splits == 1 else None, B, Hq, Hkv, C, self.splits, self.EPS, self.SCALE, s)
         if self.splits > 1:

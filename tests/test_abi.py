@@ -67,7 +67,9 @@ def test_bad_arguments_raise_without_launching():
 def test_attention_splits_policy():
     # One split from 128 (sequence, KV head) pairs at moderate context or 512 at any;
     # else about 512 workgroups (768 from 64 pairs) of >= 256 keys, 128-key splits while CUs would idle.
-    assert _lib.call("q3_attn_splits", 1, 8, 64) == 1
+    assert _lib.call("q3_attn_splits", 1, 8, 64) == 2     # two one-block splits (config 1)
+    assert _lib.call("q3_attn_splits", 1, 8, 63) == 1
+    assert _lib.call("q3_attn_splits", 4, 8, 64) == 1
     assert _lib.call("q3_attn_splits", 1, 8, 1536) == 16   # 96 keys per split
     assert _lib.call("q3_attn_splits", 1, 8, 2048) == 16   # 128 (96 would take 22)
     assert _lib.call("q3_attn_splits", 1, 8, 3000) == 24
