@@ -67,18 +67,18 @@ def prefill_figures(B: int, P: int, ms: float) -> dict:
             "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "flop": int(gemm + attn)}
 
 
-def time_layer_graph(eng, enqueue_layer, reps: int = 20) -> float:
-    """Mean device time (ms) of one launch: ``enqueue_layer(i, L)`` for every
-    layer captured as one graph on the engine's stream, replayed ``reps``
-    times between two HIP events on that stream."""
+def _graph_ms(eng, enqueue, reps: int) -> float:
+    """Mean device time (ms) of one replay of the graph that ``enqueue()``
+    captures on the engine's stream, replayed ``reps`` times between two HIP
+    events on that stream."""
     import torch
     from starter_amd._lib import call
 
     s = eng.stream.cuda_stream
     call("q3_graph_begin", s)
     try:
-        for i, L in enumerate(eng.layers):
-            enqueue_layer(i, L)
+        with torch.cuda.stream(eng.stream):
+            enqueue()
     finally:
         ex = ctypes.c_void_p()
         call("q3_graph_end", s, ctypes.byref(ex))
@@ -91,9 +91,28 @@ def time_layer_graph(eng, enqueue_layer, reps: int = 20) -> float:
             call("q3_graph_launch", ex.value, s)
         stop.record(eng.stream)
         stop.synchronize()
-        return start.elapsed_time(stop) / (reps * len(eng.layers))
+        return start.elapsed_time(stop) / reps
     finally:
         call("q3_graph_destroy", ex.value)
+
+
+def time_layer_graph(eng, enqueue_layer, reps: int = 20, clear_exchange: bool = False) -> float:
+    """Mean device time (ms) of one launch: ``enqueue_layer(i, L)`` for every
+    layer captured as one graph, timed over ``reps`` replays.  With
+    ``clear_exchange`` each replay first zeroes the fused launches' exchange
+    words, so that no launch finds words a previous replay left at the same
+    (position, layer) and every wait in it is a real one; the fill kernels' own
+    time, taken from a graph of the fills alone, is subtracted."""
+    def layers():
+        if clear_exchange:
+            eng._clear_exchange()
+        for i, L in enumerate(eng.layers):
+            enqueue_layer(i, L)
+
+    ms = _graph_ms(eng, layers, reps)
+    if clear_exchange:
+        ms -= _graph_ms(eng, eng._clear_exchange, reps)
+    return ms / len(eng.layers)
 
 
 def kernel_line(name: str, nbytes: int, ms: float, traffic_file: str) -> dict:
@@ -108,7 +127,11 @@ def kernel_rooflines(eng, wl) -> list[dict]:
 
     B <= 4: the gate/up GEMV (norm prologue, SwiGLU epilogue); bytes per launch
     are the [2I, H] BF16 weight, B rows of the residual in, B rows of I
-    activations out and the [H] gain.  B = 5..64: decode attention at the
+    activations out and the [H] gain.  At one row also the fused launch of
+    q|k|v projection, attention, split merge and o projection + residual join:
+    the q|k|v and o weights, K+V of every cached key at the current position,
+    the residual read and written, the gains and the appended key and value
+    (the gate/up rows it warms into L2 are not counted).  B = 5..64: decode attention at the
     current position (K+V of every cached key of every (sequence, KV head),
     the q|k|v rows in, the output rows out, the appended key and value) and
     the MFMA gate/up projection (weight, input rows, activations out).
@@ -131,6 +154,15 @@ def kernel_rooflines(eng, wl) -> list[dict]:
             None, 0, s))
         out.append(kernel_line("gemv_dot2 gate_up (norm prologue, SwiGLU epilogue)", gate_up + H * 2, ms,
                                f"gemv_gate_up_b{B}_traffic.txt"))
+        if eng.qkv_attn_o:
+            ctx = int(eng.g_pos.item()) + 1
+            Hkv, Hq, D = eng.KV_HEADS, eng.HEADS, eng.HEAD_DIM
+            fused = (eng.qkv_size * H * 2 + H * Hq * D * 2 + B * Hkv * ctx * D * 2 * 2 + 2 * B * H * 2
+                     + (H + 2 * D) * 2 + B * Hkv * D * 2 * 2)
+            ms = time_layer_graph(eng, eng._qkv_attn_layer, clear_exchange=True)
+            out.append(kernel_line(f"qkv_attn (q|k|v GEMV + attention + {eng.splits}-split merge + o GEMV + "
+                                   f"residual, one launch, context {ctx})", fused, ms,
+                                   f"qkv_attn_{tag}_traffic.txt"))
     elif eng.skinny:
         T = lambda w: eng.tiled[id(w)].data_ptr()  # noqa: E731
         ms = time_layer_graph(eng, lambda i, L: call(
@@ -145,7 +177,7 @@ def kernel_rooflines(eng, wl) -> list[dict]:
         kc0, vc0 = eng.cache_k.data_ptr(), eng.cache_v.data_ptr()
         ms = time_layer_graph(eng, lambda i, L: eng._attention(
             i, L, (None, eng.qkv_size, eng.skinny_ws.data_ptr(), s_qkv), kc0 + i * layer_stride,
-            vc0 + i * layer_stride))
+            vc0 + i * layer_stride), clear_exchange=eng.attn_fused)
         Hkv, Hq, D = eng.KV_HEADS, eng.HEADS, eng.HEAD_DIM
         attn = B * Hkv * ctx * D * 2 * 2 + B * eng.qkv_size * 2 + B * Hq * D * 2 + B * Hkv * D * 2 * 2
         out.append(kernel_line(f"attn_decode (split-K GQA, {eng.splits} split(s), context {ctx})", attn, ms,

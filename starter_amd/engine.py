@@ -401,15 +401,7 @@ class Engine:
                                        _ptr(self.act), _ptr(self.nbuf))
         for i, L in enumerate(self.layers):
             if self.qkv_attn:
-                first, with_o = i == 0, self.qkv_attn_o
-                call("q3_qkv_attn", _lib.X_EMBED_NORM if first else _lib.X_NORM, _ptr(self.embed) if first else resid,
-                     H, tok if first else None, _ptr(L["in_ln"]), self.EPS, resid if first or with_o else None,
-                     _ptr(L["qkv"]), H, _ptr(self.qkv_x), _ptr(L["q_norm"]), _ptr(L["k_norm"]),
-                     _ptr(self.cos_table), _ptr(self.sin_table), pos, kc0 + i * layer_stride,
-                     vc0 + i * layer_stride, _ptr(self.attn_x), None if with_o else attn,
-                     _ptr(L["o"]) if with_o else None, _ptr(self.o_x) if with_o else None,
-                     _ptr(L["gate_up"]) if with_o else None, 2 * I, self.gate_up_group,
-                     B, Hq, Hkv, C, self.splits, i, self.SCALE, _ptr(self.attn_err), s)
+                self._qkv_attn_layer(i, L)
             elif self.small:
                 if i == 0:
                     call("q3_gemv", _lib.X_EMBED_NORM, _ptr(self.embed), H, tok, _ptr(L["in_ln"]), self.EPS,
@@ -487,6 +479,24 @@ class Engine:
              V, _ptr(self.part_val), _ptr(self.part_idx), pos, *self._records(), s)
         call("q3_argmax_finish", _ptr(self.part_val), _ptr(self.part_idx), self.lm_parts, B, tok, pos,
              _ptr(self.g_counter), *self._records(), s)
+
+    def _qkv_attn_layer(self, i: int, L: dict) -> None:
+        """Layer i's q|k|v projection, attention and split merge as one launch
+        (``q3_qkv_attn``), with the o projection and its residual join at one
+        row (``qkv_attn_o``); layer 0 takes its input from the embedding."""
+        B, H, I, Hq, Hkv, C, s = (self.batch, self.HIDDEN, self.INTER, self.HEADS, self.KV_HEADS, self.capacity,
+                                  self._s)
+        layer_stride = self.cache_k[0].numel() * 2
+        first, with_o = i == 0, self.qkv_attn_o
+        resid = _ptr(self.resid)
+        call("q3_qkv_attn", _lib.X_EMBED_NORM if first else _lib.X_NORM, _ptr(self.embed) if first else resid,
+             H, _ptr(self.g_token) if first else None, _ptr(L["in_ln"]), self.EPS,
+             resid if first or with_o else None, _ptr(L["qkv"]), H, _ptr(self.qkv_x), _ptr(L["q_norm"]),
+             _ptr(L["k_norm"]), _ptr(self.cos_table), _ptr(self.sin_table), _ptr(self.g_pos),
+             self.cache_k.data_ptr() + i * layer_stride, self.cache_v.data_ptr() + i * layer_stride,
+             _ptr(self.attn_x), None if with_o else _ptr(self.attn_out), _ptr(L["o"]) if with_o else None,
+             _ptr(self.o_x) if with_o else None, _ptr(L["gate_up"]) if with_o else None, 2 * I,
+             self.gate_up_group, B, Hq, Hkv, C, self.splits, i, self.SCALE, _ptr(self.attn_err), s)
 
     def _attention(self, i: int, L: dict, src: tuple, kc: int, vc: int) -> None:
         """Layer i's decode attention into attn_out: q/k norm + RoPE + KV append,
