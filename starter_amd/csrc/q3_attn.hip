@@ -1080,7 +1080,7 @@ constexpr long PREFILL_WIDE_WGS = 512;     // 32-query workgroups from this many
 
 // grid (ceil(T/(16 CB)), Hkv, B); wave w = query head kvh*4 + w, 16 CB
 // queries per workgroup (CB MFMA column blocks of 16).  Keys advance 64 at a time through
-// two LDS stages (K and V tiles in the decode layout, kv_slot) filled by
+// two LDS stages (K tiles in the decode layout, kv_slot; V tiles in vt_slot's) filled by
 // direct global-to-LDS loads, so the four heads share each K/V byte and the
 // next block streams in while this one computes.  Per block and column block:
 // S^T = K.Q^T (16 MFMAs), the online softmax in base 2 (scores scaled by
@@ -1134,20 +1134,20 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
 
     // Direct load j of thread tid fills 16-byte slot 256j + tid of a tile:
     // key 16j + tid/16, slot position tid%16, i.e. chunk (tid%16) ^ (key & 15)
-    // (kv_slot).  Keys past key_end re-read key_end - 1 (inside the cache);
+    // of a K tile (kv_slot), chunk (tid%16) ^ (2 key & 15) of a V tile
+    // (vt_slot).  Keys past key_end re-read key_end - 1 (inside the cache);
     // every query masks them, so they add exactly zero.
     const char* kbase = reinterpret_cast<const char*>(cache_k + ((int64_t)b * Hkv + kvh) * capacity * D);
     const char* vbase = reinterpret_cast<const char*>(cache_v + ((int64_t)b * Hkv + kvh) * capacity * D);
-    const int krow = tid >> 4, kchunk = (tid & 15) ^ (krow & 15);
+    const int krow = tid >> 4, kchunk = (tid & 15) ^ (krow & 15), vchunk = (tid & 15) ^ ((2 * krow) & 15);
     const uint32_t lds_thr = q3dma::lds_address(lds) + w * 64 * 16;
     auto issue = [&](int stage, int kb) {
         const uint32_t base = lds_thr + stage * PSTAGE;
 #pragma unroll
         for (int j = 0; j < PDMA; ++j) {
             const int key = min(kb + 16 * j + krow, key_end - 1);
-            const uint32_t voff = (uint32_t)(key * D + 8 * kchunk) * 2u;
-            q3dma::load_to_lds(kbase, voff, base + j * THREADS * 16);
-            q3dma::load_to_lds(vbase, voff, base + PTILE + j * THREADS * 16);
+            q3dma::load_to_lds(kbase, (uint32_t)(key * D + 8 * kchunk) * 2u, base + j * THREADS * 16);
+            q3dma::load_to_lds(vbase, (uint32_t)(key * D + 8 * vchunk) * 2u, base + PTILE + j * THREADS * 16);
         }
     };
 
@@ -1242,7 +1242,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int dm = 0; dm < 8; ++dm) {
-                const bf16x8_t va = vt_operand_tr(vt + j * 32 * D, dm, lane);
+                const bf16x8_t va = vt_operand_tr<true>(vt + j * 32 * D, dm, lane);
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
                     acc[cb][dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][j], acc[cb][dm], 0, 0, 0);

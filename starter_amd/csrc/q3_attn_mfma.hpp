@@ -23,9 +23,16 @@ constexpr int ABLK = 32;  // keys per block
 
 // Decode K/V tiles in LDS: [32 keys][16 chunks of 16 bytes], chunk c of key r
 // stored at slot c ^ (r & 15).  Rows arrive whole (1 KB = four keys per load
-// instruction); K operand reads (16 keys at one chunk) and the transposed V
-// reads then spread over all banks.
+// instruction) and a K operand read (16 keys at one chunk) touches all 16 slot
+// positions.
 __device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
+// A transposing V read (below) is served 32 lanes per LDS cycle: 8 keys r (four
+// per lane group) at two adjacent chunks.  kv_slot puts those 16 (key, chunk)
+// pairs on 8 slot positions, two each: a two-way bank conflict on every read.
+// Chunk c of key r at c ^ (2r & 15) spreads them over all 16 (the prefill
+// attention's V tiles, which its direct loads fill in any order for free; in
+// the decode kernels the scattered writes measured no faster at one row).
+__device__ __forceinline__ int vt_slot(int r, int c) { return r * 16 + (c ^ ((2 * r) & 15)); }
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 #define Q3_LDS(p) ((__attribute__((address_space(3))) i16x4_t*)(p))
@@ -34,12 +41,15 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 // each 16-lane group, lane i names 4 consecutive d of one key (key 4*(i/4) +
 // base, d = 16dm + 4*(i%4)); the transpose hands lane n the element d = 16dm + n
 // of the four keys.  Keys 4g..4g+3 fill k slots 0-3, keys 16+4g.. slots 4-7.
+// VSW: the tile is in vt_slot's layout, else kv_slot's.
+template <bool VSW = false>
 __device__ __forceinline__ bf16x8_t vt_operand_tr(const bf16_t* vt, int dm, int lane) {
     const int g = lane >> 4, i = lane & 15;
     const int c = 2 * dm + ((i & 3) >> 1), half = (i & 1) * 4;
     const int r0 = 4 * g + (i >> 2), r1 = r0 + 16;
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r0, c) * 8 + half));
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + kv_slot(r1, c) * 8 + half));
+    const int s0 = VSW ? vt_slot(r0, c) : kv_slot(r0, c), s1 = VSW ? vt_slot(r1, c) : kv_slot(r1, c);
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + s0 * 8 + half));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(Q3_LDS(vt + s1 * 8 + half));
     typedef short i16x8_t __attribute__((ext_vector_type(8)));
     const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(bf16x8_t, v);
