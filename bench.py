@@ -117,9 +117,13 @@ def time_layer_graph(eng, enqueue_layer, reps: int = 20, clear_exchange: bool = 
 
 def kernel_line(name: str, nbytes: int, ms: float, traffic_file: str) -> dict:
     achieved = nbytes / (ms * 1e-3) / 1e9
-    return {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+    line = {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(traffic_file),
             "bytes_per_launch": int(nbytes), "us_per_launch": round(ms * 1e3, 2)}
+    note = measured_traffic(traffic_file, "traffic_note")
+    if note:
+        line["traffic_note"] = note
+    return line
 
 
 def kernel_rooflines(eng, wl) -> list[dict]:
@@ -185,16 +189,18 @@ def kernel_rooflines(eng, wl) -> list[dict]:
     return sorted(out, key=lambda k: -k["us_per_launch"])
 
 
-def measured_traffic(name: str):
+def measured_traffic(name: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary
     (``profiles/<name>``, counters scaled by a plain copy of known size), or None
-    when no such measurement exists for this kernel and workload."""
+    when no such measurement exists for this kernel and workload.  With
+    ``key="traffic_note"``: the summary's one-line reading of that figure, if any."""
     path = pathlib.Path(__file__).resolve().parent / "profiles" / name
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1])
+        if line.startswith(key + ":"):
+            value = line.split(":", 1)[1].strip()
+            return int(value) if key == "traffic_bytes_per_launch" else value
     return None
 
 
