@@ -39,8 +39,9 @@
 //   threads, BM x BN tiles of up to 128 x 128, LDS staged through registers.
 //
 // Operands: A = W rows (n), B = x rows (m), so a lane's four C values are four
-// consecutive output columns of one token row (8-byte stores; both halves of a
-// SwiGLU pair in one lane).
+// consecutive output columns of one token row (both halves of a SwiGLU pair in
+// one lane); the wide tiling regroups them across lanes for 16-byte stores
+// where the output rows allow it (store_row16).
 #include "q3_common.hpp"
 #include "q3_dma.hpp"
 #include "q3.h"
@@ -75,6 +76,65 @@ __device__ __forceinline__ void store4(bf16_t* y, int ldy, int m, int col, const
 }
 
 // ------------------------------------------------------------------ wide
+
+// One 16-row block pair of a wave's 16 x 64 output rows, stored 16 bytes per
+// lane.  After the MFMAs lane (g, n) holds four consecutive columns of each
+// 16-column block i; gfx950's cross-row swaps regroup them so that a lane
+// holds eight consecutive output columns, and each row's 64 (SwiGLU: 32)
+// output columns go out as four 16-byte stores instead of sixteen 4- or
+// 8-byte pieces (measured on MI355X at M = 131072: a 19456-wide store
+// epilogue 10.88 -> 10.39 ms, qkv 3.35 -> 3.19 ms).  Same values and rounding
+// points as store4.
+//  * v_permlane16_swap(X, Y) exchanges X's odd 16-lane rows with Y's even
+//    rows: row g of the first result holds X's or Y's row g & ~1, of the
+//    second their row g | 1.  Pairing blocks i, i+1 leaves lane g columns
+//    8 (g >> 1) .. +7 of block i + (g & 1).
+//  * v_permlane32_swap exchanges the first's rows 2-3 with the second's rows
+//    0-1.  After both swaps a SwiGLU lane g holds block g's eight outputs.
+// All lanes take part in the swaps; rows past M and columns past N are
+// masked only at the store.  Needs ldy % 8 == 0, a 16-byte aligned y and N a
+// multiple of 8 (SwiGLU: 16).
+template <int EPI>
+__device__ __forceinline__ void store_row16(const f32x4_t (&blk)[4], bf16_t* y, int ldy, int m, bool row_ok,
+                                            int c0, int N, int g) {
+    if constexpr (EPI == Q3_EPI_SWIGLU) {
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            d[i] = pack2(f2bf(silu_bf16(rbf(blk[i][0])) * rbf(blk[i][1])),
+                         f2bf(silu_bf16(rbf(blk[i][2])) * rbf(blk[i][3])));
+        const auto p01 = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
+        const auto p23 = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
+        const auto lo = __builtin_amdgcn_permlane32_swap(p01[0], p23[0], false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(p01[1], p23[1], false, false);
+        const int col = (c0 >> 1) + 8 * g;
+        if (row_ok && col < (N >> 1))
+            *reinterpret_cast<uint4*>(y + (int64_t)m * ldy + col) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+            const f32x4_t& p = blk[i];
+            const f32x4_t& q = blk[i + 1];
+            const auto s0 = __builtin_amdgcn_permlane16_swap(pack2(f2bf(p[0]), f2bf(p[1])),
+                                                             pack2(f2bf(q[0]), f2bf(q[1])), false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(pack2(f2bf(p[2]), f2bf(p[3])),
+                                                             pack2(f2bf(q[2]), f2bf(q[3])), false, false);
+            const int col = c0 + 16 * (i + (g & 1)) + 8 * (g >> 1);
+            if (row_ok && col < N) {
+                uint4* dst = reinterpret_cast<uint4*>(y + (int64_t)m * ldy + col);
+                uint4 v = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+                if constexpr (EPI == Q3_EPI_RESID) {
+                    const uint4 r = *dst;
+                    auto join = [](uint32_t rw, uint32_t vw) {
+                        return pack2(f2bf(bflo(rw) + bflo(vw)), f2bf(bfhi(rw) + bfhi(vw)));
+                    };
+                    v = make_uint4(join(r.x, v.x), join(r.y, v.y), join(r.z, v.z), join(r.w, v.w));
+                }
+                *dst = v;
+            }
+        }
+    }
+}
 
 constexpr int WIDE_THREADS = 512;
 constexpr int WIDE_BK = 64;
@@ -113,7 +173,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
                                                                     const bf16_t* __restrict__ w, int M, int N,
                                                                     int K, bf16_t* __restrict__ y, int ldy, int tm,
                                                                     int tn, int full, int splits,
-                                                                    float* __restrict__ part) {
+                                                                    float* __restrict__ part, bool vec16) {
     constexpr int WT = WIDE_TCH * 16;             // 32 KB: one operand tile
     __shared__ __align__(1024) char lds[5 * WT];  // x tiles in three stages, then W tiles in two
 
@@ -242,6 +302,17 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gemm_wide_kernel(const bf16_t
     wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
     // acc[i][j][e] = C[token m0 + 128wm + 16j + n][column n0 + 64wn + 16i + 4g + e].
+    if constexpr (EPI != EPI_PARTIAL) {
+        if (ns == 1 && vec16) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const f32x4_t blk[4] = {acc[0][j], acc[1][j], acc[2][j], acc[3][j]};
+                const int m = m0 + wm * 128 + 16 * j + n;
+                store_row16<EPI>(blk, y, ldy, m, m < M, n0 + wn * 64, N, g);
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int m = m0 + wm * 128 + 16 * j + n;
@@ -427,13 +498,16 @@ int launch(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int e
 int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, int epi, bf16_t* y, int ldy,
                 int full, int splits, float* part, hipStream_t stream) {
     const int tm = (M + 255) / 256, tn = (N + 255) / 256;
+    // Whole tiles store 16 bytes per lane where the output rows allow it.
+    const bool vec16 = y && ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+                       N % (epi == Q3_EPI_SWIGLU ? 16 : 8) == 0;
     const int tail = tm * tn - full;
     const dim3 grid(full + tail * splits);
     const bool reduce = epi != EPI_PARTIAL && tail > 0;
     if (reduce && (splits < 2 || splits > TAIL_MAX_SPLITS || !part)) return (int)hipErrorInvalidValue;
 #define Q3_WIDE(E)                                                                                               \
     Q3_LAUNCH(gemm_wide_kernel<E>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K, y, ldy, tm, tn, full, \
-              splits, part);                                                                                     \
+              splits, part, vec16);                                                                              \
     if (reduce) {                                                                                                \
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return (int)e;                                     \
         Q3_LAUNCH(wide_tail_reduce_kernel<E>, dim3(tail * 64), dim3(256), 0, stream, part, splits, tail, full,   \
@@ -451,7 +525,7 @@ int launch_wide(const bf16_t* x, int ldx, const bf16_t* w, int M, int N, int K, 
             break;
         case EPI_PARTIAL:
             Q3_LAUNCH(gemm_wide_kernel<EPI_PARTIAL>, grid, dim3(WIDE_THREADS), 0, stream, x, ldx, w, M, N, K,
-                      nullptr, 0, tm, tn, 0, splits, part);
+                      nullptr, 0, tm, tn, 0, splits, part, false);
             break;
         default:
             return (int)hipErrorInvalidValue;
