@@ -403,6 +403,30 @@ def test_gemm_wide(M, N, K, epi):
         assert_nearly_exact(out[rows, :cols], want, frac=0.06, max_ulp=2)
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 6144, 2560), (2600, 19456, 2560), (3000, 3800, 320), (4100, 2576, 576)])
+def test_gemm_wide_store_widths(M, N, K):
+    """The wide tiling stores 16 bytes per lane (lanes regrouped by cross-row
+    swaps) where the output rows allow it (ldy % 8 == 0, N % 8, SwiGLU N % 16),
+    else 8 (4 for SwiGLU): the same bits either way, every epilogue, with
+    ragged token and weight tiles; nothing past the columns is written."""
+    assert call("q3_gemm_tiles_wide", M, N) == 1
+    x, w = rnd((M, K), 1.0, M + 3), rnd((N, K), 0.02, N + K + 3)
+    xd, wd = dv(x), dv(w)
+    for epi in (_lib.EPI_STORE, _lib.EPI_RESID, _lib.EPI_SWIGLU):
+        cols = N // 2 if epi == _lib.EPI_SWIGLU else N
+        res = rnd((M, cols), 1.0, 11)
+        outs = []
+        for pad in (0, 4):  # ldy = cols (16-byte stores), cols + 4 (8-byte stores)
+            buf = dv(torch.full((M, cols + pad), 5.0, dtype=torch.bfloat16))
+            buf[:, :cols] = dv(res)
+            call("q3_gemm", P(xd), K, P(wd), M, N, K, epi, P(buf), cols + pad, S())
+            torch.cuda.synchronize()
+            out = buf.cpu()
+            assert torch.all(out[:, cols:] == 5.0)
+            outs.append(out[:, :cols])
+        assert torch.equal(outs[0], outs[1]), epi
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 2560, 4096), (1024, 2560, 9728), (300, 2560, 4096),
                                    (2049, 2560, 640), (700, 3800, 576)])
 def test_gemm_partials(M, N, K):
