@@ -406,9 +406,10 @@ def test_gemm_wide(M, N, K, epi):
 @pytest.mark.parametrize("M,N,K", [(4096, 6144, 2560), (2600, 19456, 2560), (3000, 3800, 320), (4100, 2576, 576)])
 def test_gemm_wide_store_widths(M, N, K):
     """The wide tiling stores 16 bytes per lane (lanes regrouped by cross-row
-    swaps) where the output rows allow it (ldy % 8 == 0, N % 8, SwiGLU N % 16),
-    else 8 (4 for SwiGLU): the same bits either way, every epilogue, with
-    ragged token and weight tiles; nothing past the columns is written."""
+    swaps) where the output rows allow it (ldy % 8 == 0, a 16-byte aligned
+    base, N % 8, SwiGLU N % 16), else 8 (4 for SwiGLU): the same bits either
+    way, every epilogue, with ragged token and weight tiles; nothing outside
+    the output columns is written."""
     assert call("q3_gemm_tiles_wide", M, N) == 1
     x, w = rnd((M, K), 1.0, M + 3), rnd((N, K), 0.02, N + K + 3)
     xd, wd = dv(x), dv(w)
@@ -416,15 +417,20 @@ def test_gemm_wide_store_widths(M, N, K):
         cols = N // 2 if epi == _lib.EPI_SWIGLU else N
         res = rnd((M, cols), 1.0, 11)
         outs = []
-        for pad in (0, 4):  # ldy = cols (16-byte stores), cols + 4 (8-byte stores)
-            buf = dv(torch.full((M, cols + pad), 5.0, dtype=torch.bfloat16))
+        # ldy = cols (16-byte stores); cols + 4 (8-byte stores); ldy = cols + 8 with the rows
+        # starting 8 bytes into the buffer (not 16-byte aligned: 8-byte stores).
+        for pad, off in ((0, 0), (4, 0), (8, 4)):
+            flat = dv(torch.full((M * (cols + pad) + off,), 5.0, dtype=torch.bfloat16))
+            buf = flat[off:].view(M, cols + pad)
             buf[:, :cols] = dv(res)
             call("q3_gemm", P(xd), K, P(wd), M, N, K, epi, P(buf), cols + pad, S())
             torch.cuda.synchronize()
-            out = buf.cpu()
+            out = flat.cpu()
+            assert torch.all(out[:off] == 5.0)
+            out = out[off:].view(M, cols + pad)
             assert torch.all(out[:, cols:] == 5.0)
             outs.append(out[:, :cols])
-        assert torch.equal(outs[0], outs[1]), epi
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2]), epi
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 2560, 4096), (1024, 2560, 9728), (300, 2560, 4096),
