@@ -1,6 +1,7 @@
 """Decode throughput of the MI355X Qwen3-4B engine on one GPU.
 
     python bench.py [--steps K] [--warmup W] [--config 2] [--extra-configs 1,3,4,5] [--gpus 1]
+    python bench.py --kernel {gemm_gate_up,gemm_qkv,gemm_o,gemm_down,attn_prefill} --config N [--launches L]
 
 A step is one decode step of the whole batch (one token per sequence): one
 replay of the captured hipGraph.  The headline workload is BASELINE config 2
@@ -331,6 +332,68 @@ def copy_probe(nbytes: int = 1 << 30) -> int:
     return 0
 
 
+#: The prompt-pass kernels ``--kernel`` runs alone at a config's shape, for
+#: rocprofv3 counter passes: the four projections (q3_gemm_ws with their
+#: epilogues) and the causal attention.  Synthetic operands (N(0,1)
+#: activations, N(0,0.02) weights); the config gives the token count.
+KERNELS = ("gemm_gate_up", "gemm_qkv", "gemm_o", "gemm_down", "attn_prefill")
+
+
+def kernel_probe(name: str, config: int, launches: int) -> int:
+    """Run one prompt-pass kernel at config ``config``'s shape: one untimed
+    launch, then ``launches`` launches timed with HIP events (each printed).
+    ``rocprofv3 --pmc ... -- python3 bench.py --kernel NAME --config N``
+    then reads the kernel's counters per dispatch."""
+    import torch
+
+    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent))
+    from starter_amd import _lib
+    from starter_amd._lib import call
+    from starter_amd.workloads import MODEL, WORKLOADS
+
+    wl = WORKLOADS[config]
+    B, T = wl.batch, wl.prompt
+    M, H, I = B * T, MODEL.hidden_size, MODEL.intermediate_size
+    Hq, Hkv, D = MODEL.num_attention_heads, MODEL.num_key_value_heads, MODEL.head_dim
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(config)
+    stream = torch.cuda.current_stream().cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+    if name.startswith("gemm_"):
+        N, K, epi = {"gemm_gate_up": (2 * I, H, _lib.EPI_SWIGLU), "gemm_qkv": ((Hq + 2 * Hkv) * D, H, _lib.EPI_STORE),
+                     "gemm_o": (H, Hq * D, _lib.EPI_RESID), "gemm_down": (H, I, _lib.EPI_RESID)}[name]
+        x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        w = (0.02 * torch.randn(N, K, device=dev, generator=g)).bfloat16()
+        cols = N // 2 if epi == _lib.EPI_SWIGLU else N
+        y = torch.randn(M, cols, device=dev, generator=g).bfloat16()
+        ws = torch.empty(max(call("q3_gemm_ws_floats", M, N, K), 4), dtype=torch.float32, device=dev)
+        flop = 2.0 * M * N * K
+        run = lambda: call("q3_gemm_ws", P(x), K, P(w), M, N, K, epi, P(y), cols, P(ws), stream)  # noqa: E731
+        what = f"q3_gemm_ws M={M} N={N} K={K} epi={epi}"
+    elif name == "attn_prefill":
+        q = torch.randn(B, T, Hq, D, device=dev, generator=g).bfloat16()
+        k = torch.randn(B, Hkv, T, D, device=dev, generator=g).bfloat16()
+        v = torch.randn(B, Hkv, T, D, device=dev, generator=g).bfloat16()
+        out = torch.empty_like(q)
+        flop = 4.0 * D * Hq * B * T * (T + 1) / 2
+        run = lambda: call("q3_attn_prefill", P(q), P(k), P(v), P(out), B, T, 0, Hq, Hkv, T,  # noqa: E731
+                           D ** -0.5, stream)
+        what = f"q3_attn_prefill B={B} T={T} start=0"
+    else:
+        raise SystemExit(f"--kernel must be one of {', '.join(KERNELS)}")
+    run()
+    torch.cuda.synchronize()
+    for i in range(launches):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        log(f"{what}: launch {i}: {ms:.3f} ms, {flop / ms / 1e9:.0f} TFLOP/s")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +407,10 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (3 times): the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--kernel", choices=KERNELS,
+                    help="only run one prompt-pass kernel at --config's shape (an untimed launch, then "
+                         "--launches timed ones): the program rocprofv3's counter passes profile")
+    ap.add_argument("--launches", type=int, default=1)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -351,6 +418,8 @@ def main() -> int:
         return 2
     if args.copy_probe:
         return copy_probe()
+    if args.kernel:
+        return kernel_probe(args.kernel, args.config, args.launches)
 
     sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent))
     import torch
