@@ -294,8 +294,9 @@ int q3_qkv_attn(int x_mode, const uint16_t *x, int ldx, const int64_t *ids, cons
 int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K, int with_o);
 
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
- * against cache keys 0..start+T-1; out [B*T, Hq*128].  SDPA is_causal /
- * chunk mask (engine.py:263-280,777-787). */
+ * against cache keys 0..start+T-1; out [B*T, Hq*128]; q and the caches
+ * 16-byte, out 8-byte aligned.  SDPA is_causal / chunk mask
+ * (engine.py:263-280,777-787). */
 int q3_attn_prefill(const uint16_t *q, const uint16_t *cache_k, const uint16_t *cache_v,
                     uint16_t *out, int B, int T, int start, int Hq, int Hkv,
                     int capacity, float scale, hipStream_t stream);

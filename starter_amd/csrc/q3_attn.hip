@@ -1629,6 +1629,8 @@ extern "C" int q3_attn_prefill(const bf16_t* q, const bf16_t* cache_k, const bf1
                                int B, int T, int start, int Hq, int Hkv, int capacity, float scale,
                                hipStream_t stream) {
     if (B < 1 || T < 1 || start < 0 || Hq != GROUP * Hkv || start + T > capacity) return (int)hipErrorInvalidValue;
+    if ((((uintptr_t)q | (uintptr_t)cache_k | (uintptr_t)cache_v) & 15) || ((uintptr_t)out & 7))
+        return (int)hipErrorInvalidValue;
     // One (sequence, KV head) cache row block lies within 32-bit byte offsets.
     if ((int64_t)capacity * D * 2 > INT32_MAX) return (int)hipErrorInvalidValue;
     // 32 queries per workgroup (each K/V block serves two column blocks), or
