@@ -293,6 +293,29 @@ int q3_qkv_attn(int x_mode, const uint16_t *x, int ldx, const int64_t *ids, cons
                 float scale, int *err, hipStream_t stream);
 int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits, int K, int with_o);
 
+/* q3_qkv_attn at one row with the o projection (X_NORM on resid), preceded in
+ * the same launch by the previous layer's down projection and its residual
+ * join: resid' = bf16(resid + bf16(act . W_down^T)), the bits q3_gemv
+ * (X_PLAIN, EPI_RESID) stores, handed to this layer's norm and o join as
+ * flagged words rx [q3_down_rx_words(K)] (zeroed with the other exchange words
+ * before positions can repeat).  resid then holds the residual after this
+ * layer's o join, as after q3_gemv(down) then q3_qkv_attn.  W_down is [K, I];
+ * act [I]; act, W_down, rx, w, norm_w, xbuf, w_o, o_x 16-byte aligned.
+ * Applies when q3_down_qkv_attn_grid(Hq, Hkv, capacity, splits, K, I) > 0
+ * (the whole grid resident at once).  Replaces engine/engine.py:735's down
+ * _linear and the residual add that follows it (:736) together with the next
+ * layer's first half of _block (q3_qkv_attn above): one kernel boundary fewer
+ * per layer. */
+int q3_down_qkv_attn(const uint16_t *act, const uint16_t *w_down, int I, uint32_t *rx, uint16_t *resid,
+                     const uint16_t *norm_w, float eps, const uint16_t *w, int K, uint32_t *qkv_x,
+                     const uint16_t *q_norm_w, const uint16_t *k_norm_w, const uint16_t *cos_table,
+                     const uint16_t *sin_table, const int64_t *pos, uint16_t *cache_k, uint16_t *cache_v,
+                     uint32_t *xbuf, const uint16_t *w_o, uint32_t *o_x, const uint16_t *next_w, int next_rows,
+                     int next_group, int Hq, int Hkv, int capacity, int splits, int layer, float scale, int *err,
+                     hipStream_t stream);
+int q3_down_qkv_attn_grid(int Hq, int Hkv, int capacity, int splits, int K, int I);
+int q3_down_rx_words(int K);
+
 /* Causal prefill attention: q [B*T, Hq, 128] at positions start..start+T-1
  * against cache keys 0..start+T-1; out [B*T, Hq*128]; q and the caches
  * 16-byte, out 8-byte aligned.  SDPA is_causal / chunk mask

@@ -63,6 +63,10 @@ SIGNATURES = {
     "q3_qkv_attn": [_I, _P, _I, _P, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                     _I, _I, _I, _I, _I, _I, _F, _P, _P],
     "q3_qkv_attn_grid": [_I, _I, _I, _I, _I, _I, _I],
+    "q3_down_qkv_attn": [_P, _P, _I, _P, _P, _P, _F, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                         _I, _I, _I, _I, _I, _I, _F, _P, _P],
+    "q3_down_qkv_attn_grid": [_I, _I, _I, _I, _I, _I],
+    "q3_down_rx_words": [_I],
     "q3_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "q3_argmax_finish": [_P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P],
     "q3_argmax_rows": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P],
@@ -75,7 +79,7 @@ _RESTYPES = {"q3_error_string": ctypes.c_char_p}
 
 #: entry points that return a count, not an error code
 _COUNTS = {"q3_gemv_partials", "q3_attn_splits", "q3_attn_fused_grid", "q3_attn_xbuf_words", "q3_qkv_attn_grid",
-           "q3_attn_pair_grid",
+           "q3_attn_pair_grid", "q3_down_qkv_attn_grid", "q3_down_rx_words",
            "q3_skinny_splits", "q3_skinny_ws_floats", "q3_skinny_scratch_floats", "q3_gemm_tiles_wide",
            "q3_gemm_splits", "q3_gemm_ws_floats"}
 

@@ -251,14 +251,23 @@ __device__ __forceinline__ void decode_block(WaveState& st, const KVRegs& r, bf1
 // leaves its record there as flagged words; this unit folds it into its own
 // partial exactly as attn_merge_kernel folds two splits and writes the
 // normalised output (the wait is bounded: 1 s, then *a.err).
-template <int WAVES, int QP, class Mid = NoMid>
+template <int WAVES, int QP, class Mid = NoMid, bool POOL = false>
 __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kvh, int b, uint32_t* xbuf, uint32_t F,
-                                          Mid mid = Mid(), const uint32_t* partner = nullptr) {
+                                          Mid mid = Mid(), const uint32_t* partner = nullptr,
+                                          bf16_t* pool = nullptr) {
     static_assert(WAVES == 4 || WAVES == 8, "four or eight waves");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
 
-    __shared__ __align__(16) bf16_t tiles[WAVES][2][BLK * D];  // per wave: K tile, V tile
+    // Per wave a K tile then a V tile, BLK * D each: the unit's own LDS, or
+    // (POOL) the kernel's `pool`, which other roles of that kernel also use.
+    bf16_t* tiles;
+    if constexpr (POOL) {
+        tiles = pool;
+    } else {
+        __shared__ __align__(16) bf16_t own[WAVES * 2 * BLK * D];
+        tiles = own;
+    }
     __shared__ __align__(16) bf16_t qs[GROUP][D];
     __shared__ __align__(16) bf16_t knew[D];
     __shared__ __align__(16) bf16_t vnew[D];
@@ -347,8 +356,8 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
     st.l = 0.f;
 #pragma unroll
     for (int dm = 0; dm < 8; ++dm) st.acc[dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    bf16_t* kt = tiles[w][0];
-    bf16_t* vt = tiles[w][1];
+    bf16_t* kt = tiles + w * 2 * BLK * D;
+    bf16_t* vt = kt + BLK * D;
 
     if (first < end) {
         // Q^T operands, one per 32-wide slice of d: Q[n][32kk + 8g + t].
@@ -386,7 +395,7 @@ __device__ __forceinline__ void attn_unit(const DecodeArgs& a, int split, int kv
 
     // Merge the waves (lane n < 4 holds head n: O^T[16dm + 4g + i][n]); each
     // wave parks its accumulator in its own K tile.
-    float* macc = reinterpret_cast<float*>(tiles[0][0]);  // [WAVES][GROUP][D], wave w inside tiles[w]
+    float* macc = reinterpret_cast<float*>(tiles);  // [WAVES][GROUP][D], wave w inside its own tiles
     constexpr int WSTRIDE = 2 * BLK * D / 2;              // floats per wave region
     if (n < GROUP) {
         if (g == 0) { mm[w][n] = st.m; ll[w][n] = st.l; }
@@ -645,7 +654,62 @@ struct QkvGemvArgs {
     const bf16_t* w;       // weights [N, K]
     int N;
     uint32_t* qx;          // outputs as flagged words [M, N]
+    // X_WORDS: the one input row as flagged words [K] from the down workgroups
+    // of the same launch, then their n_done done words.
+    const uint32_t* xw = nullptr;
+    int n_done = 0;
+    int* err = nullptr;
 };
+
+// Input mode of the fused launch beside q3.h's X_* modes: X_NORM over one row
+// that the launch's own down workgroups hand over as flagged words.
+constexpr int X_WORDS = 3;
+
+// X_WORDS: wait for the input row's words (first the down workgroups' done
+// words, polled by wave 0 alone, then every word this thread stages, until
+// all carry flag F) and return them as the BF16 chunks qkv_rows stages:
+// chunk j of this thread is elements 8c .. 8c + 7, c = min(tid + 256 j,
+// 64 KU - 1).  Every wave of the workgroup calls it (it synchronises the
+// workgroup).  Bounded (1 s per phase, then *err and the payloads as they are).
+template <int KU, int XC>
+__device__ __forceinline__ void x_words(const QkvGemvArgs& g, uint32_t F, u32x4_t (&xv)[XC][1]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t Fs = F << 16;
+    q3x::SpinBound sb;
+    bool ok = true;
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0) {  // a scalar branch (a divergent one costs registers)
+        const auto rd = q3x::rsrc(g.xw + 64 * 8 * KU);
+        for (;;) {
+            const u32x4_t v = q3x::ld_coh(rd, 16 * min(lane, g.n_done / 4 - 1));
+            if (__all(q3x::unflagged(v, Fs) == 0)) break;
+            __builtin_amdgcn_s_sleep(2);
+            if (!sb.ok(q3x::SPIN_LIMIT)) {
+                ok = false;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const auto rs = q3x::rsrc(g.xw);
+    for (;;) {
+        uint32_t bad = 0;
+#pragma unroll
+        for (int j = 0; j < XC; ++j) {
+            const int c = min(tid + j * 256, 64 * KU - 1);
+            const u32x4_t lo = q3x::ld_coh(rs, 32 * c), hi = q3x::ld_coh(rs, 32 * c + 16);
+            bad |= q3x::unflagged(lo, Fs) | q3x::unflagged(hi, Fs);
+            xv[j][0] = u32x4_t{q3x::bfpair(lo.x, lo.y), q3x::bfpair(lo.z, lo.w), q3x::bfpair(hi.x, hi.y),
+                               q3x::bfpair(hi.z, hi.w)};
+        }
+        if (__all(bad == 0) || !ok) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (!sb.ok(q3x::SPIN_LIMIT)) {
+            ok = false;
+            break;
+        }
+    }
+    if (!ok && g.err != nullptr && lane == 0) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ float dot8v(u32x4_t a, u32x4_t b, float c) {
     c = dot2(a.x, b.x, c);
@@ -666,6 +730,7 @@ __device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_
     constexpr int XC = (64 * KU + 255) / 256;  // 16-byte input chunks per thread
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    static_assert(XMODE != X_WORDS || M == 1, "flagged input words carry one row");
     u32x4_t xv[XC][M], gv[XC];
     const bf16_t* src[M];
 #pragma unroll
@@ -677,8 +742,10 @@ __device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_
     for (int j = 0; j < XC; ++j) {
         const int c = min(tid + j * 256, 64 * KU - 1);  // past the row: a duplicate, never used
         gv[j] = *reinterpret_cast<const u32x4_t*>(g.norm_w + c * 8);
+        if constexpr (XMODE != X_WORDS) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(src[m] + c * 8);
+            for (int m = 0; m < M; ++m) xv[j][m] = *reinterpret_cast<const u32x4_t*>(src[m] + c * 8);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // Unconditional weight loads (a row past the last re-reads the last row
@@ -693,6 +760,7 @@ __device__ __forceinline__ void qkv_rows(const QkvGemvArgs& g, int row0, uint32_
         for (int r = 0; r < R; ++r)
             wv[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow[r] + u * 512));
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XMODE == X_WORDS) x_words<KU, XC>(g, F, xv);
 
     float ss[M];
 #pragma unroll
@@ -794,6 +862,9 @@ struct OprojArgs {
     const bf16_t* nw;
     int nrows, ngroup;
     uint32_t* sink;
+    // X_WORDS launches: the residual the join starts from, as the down
+    // workgroups' flagged words [N] (resid is then only written).
+    const uint32_t* rx = nullptr;
 };
 constexpr int WARM_BYTES = 1024;
 // o rows per wave: QO_RN on the workgroups that are neither attention units
@@ -906,15 +977,124 @@ __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+    // X_WORDS: the residual words of this wave's rows.  Every input word of
+    // the launch's q|k|v rows carried flag F before any attention unit could
+    // start, so these do too; the wait is kept (bounded) rather than assumed.
+    uint32_t wd = 0;
+    if constexpr (XMODE == X_WORDS) {
+        const auto rr = q3x::rsrc(o.rx);
+        const int nn = min(row0 + min(lane, R - 1), o.N - 1);
+        for (;;) {
+            wd = __builtin_amdgcn_raw_buffer_load_b32(rr, 4 * nn, 0, q3x::SC1);
+            if (__all((wd >> 16) == F) || !ok) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (!sb.ok(q3x::SPIN_LIMIT)) ok = false;
+        }
+        if (!ok && err != nullptr && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (lane < R && row0 + lane < o.N) {
         float v = 0.f;
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (r == lane) v = acc[r];
         const int n = row0 + lane;
-        const bf16_t old = XMODE == Q3_X_EMBED_NORM ? o.table[o.ids[0] * (int64_t)o.N + n] : o.resid[n];
+        bf16_t old;
+        if constexpr (XMODE == Q3_X_EMBED_NORM) {
+            old = o.table[o.ids[0] * (int64_t)o.N + n];
+        } else if constexpr (XMODE == X_WORDS) {
+            old = (bf16_t)(wd & 0xffffu);
+        } else {
+            old = o.resid[n];
+        }
         o.resid[n] = (bf16_t)f2bf(bf2f(old) + rbf(v));
     }
+}
+
+// The previous layer's down projection with its residual join, at one row of
+// input, run first by every workgroup of an X_WORDS launch (n_down = the
+// grid): resid'[n] = bf16(resid[n] + bf16(sum_k W_down[n, k] * act[k])),
+// stored as flagged words rx[n] for this launch's q|k|v norm and o join; then
+// each workgroup's done word rx[H + dg].  Arithmetic and order are those of
+// gemv_dot2_kernel (X_PLAIN from LDS, EPI_RESID), so rx carries the bits
+// q3_gemv would store.  Workgroup dg takes rows dg + n_down j < H (j < rpw,
+// 8..12 of them), wave w those with j = w + 4 i: the first two rows' weights
+// are in flight before the input is staged, a third follows their sums.  A
+// CU streams its down rows before its q|k|v rows, which then wait for every
+// workgroup's down rows while their own weights stream.
+struct DownArgs {
+    const bf16_t* w;      // W_down [H, 512 KUD]
+    const bf16_t* act;    // its input row [512 KUD] (written by an earlier launch)
+    const bf16_t* resid;  // the residual before the join [H] (written by an earlier launch)
+    uint32_t* rx;         // [H] joined residual as flagged words, then [n_down] done words
+    int H;
+};
+
+template <int KUD>
+__device__ __forceinline__ void down_unit(const DownArgs& d, int dg, int n_down, uint32_t F, bf16_t* xs) {
+    constexpr int K = 512 * KUD;
+    constexpr int XC = (64 * KUD + 255) / 256;  // 16-byte input chunks per thread
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rpw = (d.H - dg + n_down - 1) / n_down;
+    const int nr = (rpw - w + 3) >> 2;  // this wave's rows (2 or 3)
+    const int r0 = dg + n_down * w, r1 = dg + n_down * (w + 4), r2 = min(dg + n_down * (w + 8), d.H - 1);
+
+    // Waves whose rows are stored; the last one stores the done word, so no
+    // wave waits for another before its q|k|v weights (the attention tiles
+    // that reuse this LDS are written only after later workgroup barriers).
+    __shared__ uint32_t waves_done;
+    if (tid == 0) waves_done = 0;
+    u32x4_t xv[XC];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = min(tid + j * 256, 64 * KUD - 1);  // past the row: a duplicate, never used
+        xv[j] = *reinterpret_cast<const u32x4_t*>(d.act + c * 8);
+    }
+    const bf16_t old = d.resid[lane < nr ? dg + n_down * (w + 4 * lane) : r0];  // lane i < nr: row i's
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4_t wa[KUD], wb[KUD];
+#pragma unroll
+    for (int u = 0; u < KUD; ++u) {
+        wa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(d.w + (int64_t)r0 * K + lane * 8 + u * 512));
+        wb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(d.w + (int64_t)r1 * K + lane * 8 + u * 512));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = tid + j * 256;
+        if (c < 64 * KUD) *reinterpret_cast<u32x4_t*>(xs + c * 8) = xv[j];
+    }
+    __syncthreads();
+
+    // The first two rows in one pass (each input chunk read from LDS once).
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < KUD; ++u) {
+        const u32x4_t xc = *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512);
+        acc0 = dot8v(wa[u], xc, acc0);
+        acc1 = dot8v(wb[u], xc, acc1);
+    }
+    // Their sums first, and nothing moved across: otherwise the third row's
+    // loads get registers of their own next to wa's and spill.
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nr == 3) {
+#pragma unroll
+        for (int u = 0; u < KUD; ++u)
+            wa[u] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4_t*>(d.w + (int64_t)r2 * K + lane * 8 + u * 512));
+#pragma unroll
+        for (int u = 0; u < KUD; ++u)
+            acc2 = dot8v(wa[u], *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512), acc2);
+    }
+    acc2 = wave_sum(acc2);
+    if (lane < nr) {
+        const float v = lane == 0 ? acc0 : lane == 1 ? acc1 : acc2;
+        q3x::st_coh32(d.rx + dg + n_down * (w + 4 * lane), q3x::word(f2bf(bf2f(old) + rbf(v)), F));
+    }
+    // A hint only: readers check every row word's own flag.
+    if (lane == 0 && atomicAdd(&waves_done, 1u) == 3u) q3x::st_coh32(d.rx + d.H + dg, q3x::word(0, F));
 }
 
 // Grid: max(projection workgroups, attention + merge workgroups + the o
@@ -923,16 +1103,24 @@ __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32
 // wait is still bounded (1 s, then *err).  With the o projection (KUO > 0, one
 // row of input): workgroup n_att + n_mrg + j (j < n_on) takes o rows 16 j ..
 // 16 j + 15, and attention workgroup i (i < n_oa) rows 16 n_on + 8 i .. + 7.
-template <int M, int KU, int XMODE, int RA, int RO, int KUO>
-__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeArgs a, OprojArgs o, uint32_t* xbuf,
-                                                         int layer, int n_gemv, int n_on, int n_oa) {
+// X_WORDS (KUD > 0): every workgroup first runs its share of the previous
+// layer's down projection (down_unit, n_down = the grid), then its roles.
+template <int M, int KU, int XMODE, int RA, int RO, int KUO, int KUD>
+__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeArgs a, OprojArgs o, DownArgs dn,
+                                                         uint32_t* xbuf, int layer, int n_gemv, int n_on, int n_oa,
+                                                         int n_down) {
     static_assert(KUO == 0 || M == 1, "the fused o projection takes one row");
+    static_assert((XMODE == X_WORDS) == (KUD > 0) && (KUD == 0 || KUO > 0), "down rows precede q|k|v and o");
     constexpr int XS = M * 512 * KU > 512 * KUO ? M * 512 * KU : 512 * KUO;
     __shared__ __align__(16) bf16_t xs[XS];
     __shared__ float red[4][M];
+    // The attention units' K/V tiles; the down rows' staged input.
+    __shared__ __align__(16) bf16_t pool[4 * 2 * BLK * D];
+    static_assert(KUD * 512 <= 4 * 2 * BLK * D, "the down input fits the tile pool");
     const int n_att = a.splits * a.Hkv * a.B;
     const int n_mrg = a.Hq / 2 * a.B;
     const uint32_t F = step_flag((int)*a.pos, layer);
+    if constexpr (KUD > 0) down_unit<KUD>(dn, blockIdx.x, n_down, F, pool);
     const int bid = blockIdx.x, wave = threadIdx.x >> 6;
     const auto gemv = [&]() {
         if (bid >= n_gemv) return;
@@ -941,7 +1129,7 @@ __global__ __launch_bounds__(256, 2) void qkv_attn_kernel(QkvGemvArgs g, DecodeA
     };
     if (bid < n_att) {
         const int split = bid % a.splits, kvh = (bid / a.splits) % a.Hkv, b = bid / (a.splits * a.Hkv);
-        attn_unit<4, 3>(a, split, kvh, b, xbuf, F, gemv);
+        attn_unit<4, 3, decltype(gemv), true>(a, split, kvh, b, xbuf, F, gemv, nullptr, pool);
         if constexpr (KUO > 0) {
             if (bid < n_oa) {
                 const int row0 = 16 * n_on + (bid * 4 + wave) * QO_RA;
@@ -1514,16 +1702,21 @@ static QaPlan qa_plan(int B, int Hq, int Hkv, int splits, int K, bool with_o) {
     return p;
 }
 
-template <int M, int KU, int XMODE, int RA, int RO, int KUO>
+template <int M, int KU, int XMODE, int RA, int RO, int KUO, int KUD = 0>
 static const void* qkv_attn_fn() {
-    return reinterpret_cast<const void*>(qkv_attn_kernel<M, KU, XMODE, RA, RO, KUO>);
+    return reinterpret_cast<const void*>(qkv_attn_kernel<M, KU, XMODE, RA, RO, KUO, KUD>);
 }
 
-// The fused kernel for (rows, K, input mode, row split, o width / 512), or
-// null outside what it is built for.
-static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra, int kuo) {
+// The fused kernel for (rows, K, input mode, row split, o width / 512, down
+// width / 512), or null outside what it is built for.
+static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra, int kuo, int kud) {
     const bool emb = x_mode == Q3_X_EMBED_NORM;
-    if (x_mode != Q3_X_NORM && !emb) return nullptr;
+    if (x_mode == X_WORDS) {
+        if (M == 1 && K == 2560 && ra == 5 && kuo == 8 && kud == 19) return qkv_attn_fn<1, 5, X_WORDS, 5, 7, 8, 19>();
+        if (M == 1 && K == 512 && ra == 6 && kuo == 2 && kud == 2) return qkv_attn_fn<1, 1, X_WORDS, 6, 6, 2, 2>();
+        return nullptr;
+    }
+    if ((x_mode != Q3_X_NORM && !emb) || kud != 0) return nullptr;
 #define Q3_QA(MV, KUV, RAV, ROV, KUOV)                                                                     \
     if (M == MV && K == 512 * KUV && ra == RAV && kuo == KUOV)                                             \
         return emb ? qkv_attn_fn<MV, KUV, Q3_X_EMBED_NORM, RAV, ROV, KUOV>()                               \
@@ -1540,19 +1733,21 @@ static const void* qkv_attn_kernel_for(int M, int K, int x_mode, int ra, int kuo
     return nullptr;
 }
 
-// Workgroups of the fused kernel resident at once on the current device, for
-// both input modes (0 if unknown).  Cached per device and kernel.
-static int qkv_attn_resident(int M, int K, int ra, int kuo) {
+// Workgroups of the fused kernel resident at once on the current device (0
+// if unknown): for both the X_NORM and X_EMBED_NORM kernels, or (kud > 0) the
+// X_WORDS one.  Cached per device and kernel.
+static int qkv_attn_resident(int M, int K, int ra, int kuo, int kud) {
     constexpr int MAX_DEV = 64;
-    static int cached[MAX_DEV][2][2][2][3];  // 0 = not yet asked; -1 = unknown
+    static int cached[MAX_DEV][2][2][2][3][2];  // 0 = not yet asked; -1 = unknown
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
-    int& c = cached[dev][M - 1][K == 2560 ? 1 : 0][ra == 5 ? 1 : 0][kuo == 0 ? 0 : kuo == 2 ? 1 : 2];
+    int& c = cached[dev][M - 1][K == 2560 ? 1 : 0][ra == 5 ? 1 : 0][kuo == 0 ? 0 : kuo == 2 ? 1 : 2][kud ? 1 : 0];
     if (c != 0) return c > 0 ? c : 0;
     int cus = 0, per = 1 << 30;
     bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
-    for (int xm : {Q3_X_NORM, Q3_X_EMBED_NORM}) {
-        const void* fn = qkv_attn_kernel_for(M, K, xm, ra, kuo);
+    const int modes[2] = {kud ? X_WORDS : Q3_X_NORM, kud ? X_WORDS : Q3_X_EMBED_NORM};
+    for (int xm : modes) {
+        const void* fn = qkv_attn_kernel_for(M, K, xm, ra, kuo, kud);
         int n = 0;
         ok = ok && fn != nullptr && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) == hipSuccess;
         per = n < per ? n : per;
@@ -1575,7 +1770,39 @@ extern "C" int q3_qkv_attn_grid(int B, int Hq, int Hkv, int capacity, int splits
     if (with_o && kuo == 0) return 0;
     if (q3_attn_fused_grid(B, Hq, Hkv, capacity, splits) == 0) return 0;
     const QaPlan p = qa_plan(B, Hq, Hkv, splits, K, with_o != 0);
-    return p.grid <= qkv_attn_resident(B, K, p.ra, kuo) ? p.grid : 0;
+    return p.grid <= qkv_attn_resident(B, K, p.ra, kuo, 0) ? p.grid : 0;
+}
+
+// Down width / 512 of the X_WORDS launch for hidden size K (0: not built).
+static int down_kud(int K, int I) { return (K == 2560 && I == 9728) ? 19 : (K == 512 && I == 1024) ? 2 : 0; }
+
+extern "C" int q3_down_rx_words(int K) { return K + 256; }
+
+extern "C" int q3_down_qkv_attn_grid(int Hq, int Hkv, int capacity, int splits, int K, int I) {
+    const int kud = down_kud(K, I);
+    if (kud == 0 || q3_qkv_attn_grid(1, Hq, Hkv, capacity, splits, K, 1) == 0) return 0;
+    const QaPlan p = qa_plan(1, Hq, Hkv, splits, K, true);
+    // Built for the row split of up to 38 splits at K = 2560 (five rows per
+    // attention wave; the six-row split would spill registers), and for grids
+    // that deal the down rows 8..12 to a workgroup (done words: at most 256).
+    if ((K == 2560 && p.ra != 5) || K / p.grid < 8 || (K + p.grid - 1) / p.grid > 12 || p.grid > 256) return 0;
+    return p.grid <= qkv_attn_resident(1, K, p.ra, qkv_attn_kuo(1, Hq, K), kud) ? p.grid : 0;
+}
+
+// One launch of qkv_attn_kernel for the arguments the entry points checked.
+static int qkv_attn_launch(int x_mode, const QkvGemvArgs& g, const DecodeArgs& a, const OprojArgs& o,
+                           const DownArgs& dn, int kud, int n_down, uint32_t* xbuf, int layer, int K, int grid,
+                           hipStream_t stream) {
+    const bool with_o = o.w != nullptr;
+    const QaPlan p = qa_plan(a.B, a.Hq, a.Hkv, a.splits, K, with_o);
+    const void* fn = qkv_attn_kernel_for(a.B, K, x_mode, p.ra, with_o ? qkv_attn_kuo(a.B, a.Hq, K) : 0, kud);
+    if (fn == nullptr) return (int)hipErrorInvalidValue;
+    int n_gemv = p.n_gemv, n_on = p.n_on, n_oa = p.n_oa;
+    void* args[] = {(void*)&g,     (void*)&a,      (void*)&o,    (void*)&dn,   (void*)&xbuf,
+                    (void*)&layer, (void*)&n_gemv, (void*)&n_on, (void*)&n_oa, (void*)&n_down};
+    (void)hipGetLastError();
+    const hipError_t rc = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+    return rc != hipSuccess ? (int)rc : (int)hipGetLastError();
 }
 
 extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* ids, const bf16_t* norm_w,
@@ -1608,14 +1835,39 @@ extern "C" int q3_qkv_attn(int x_mode, const bf16_t* x, int ldx, const int64_t* 
                  nullptr, nullptr, out, Hq, Hkv, capacity, splits, eps, scale, B, qkv_x, err, with_o ? o_x : nullptr};
     const OprojArgs o{w_o, K, with_o ? resid_out : nullptr, emb ? x : nullptr, ids, o_x, next_w, next_rows,
                       next_group, nullptr};
-    const QaPlan p = qa_plan(B, Hq, Hkv, splits, K, with_o);
-    const void* fn = qkv_attn_kernel_for(B, K, x_mode, p.ra, with_o ? qkv_attn_kuo(B, Hq, K) : 0);
-    int n_gemv = p.n_gemv, n_on = p.n_on, n_oa = p.n_oa;
-    void* args[] = {(void*)&g, (void*)&a, (void*)&o,     (void*)&xbuf,
-                    (void*)&layer, (void*)&n_gemv, (void*)&n_on, (void*)&n_oa};
-    (void)hipGetLastError();
-    const hipError_t rc = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
-    return rc != hipSuccess ? (int)rc : (int)hipGetLastError();
+    return qkv_attn_launch(x_mode, g, a, o, DownArgs{}, 0, 0, xbuf, layer, K, grid, stream);
+}
+
+extern "C" int q3_down_qkv_attn(const bf16_t* act, const bf16_t* w_down, int I, uint32_t* rx, bf16_t* resid,
+                                const bf16_t* norm_w, float eps, const bf16_t* w, int K, uint32_t* qkv_x,
+                                const bf16_t* q_norm_w, const bf16_t* k_norm_w, const bf16_t* cos_table,
+                                const bf16_t* sin_table, const int64_t* pos, bf16_t* cache_k, bf16_t* cache_v,
+                                uint32_t* xbuf, const bf16_t* w_o, uint32_t* o_x, const bf16_t* next_w,
+                                int next_rows, int next_group, int Hq, int Hkv, int capacity, int splits, int layer,
+                                float scale, int* err, hipStream_t stream) {
+    const int grid = q3_down_qkv_attn_grid(Hq, Hkv, capacity, splits, K, I);
+    const int kud = down_kud(K, I), n_down = grid;
+    if (grid == 0 || layer < 0 || layer >= 64 || !act || !w_down || !rx || !resid || !norm_w || !w || !qkv_x ||
+        !q_norm_w || !k_norm_w || !cos_table || !sin_table || !pos || !cache_k || !cache_v || !xbuf || !w_o ||
+        !o_x ||
+        (next_w && (next_group < 1 || next_rows < next_group || (next_rows % next_group) != 0 ||
+                    (reinterpret_cast<uintptr_t>(next_w) & 3) || K * 2 < WARM_BYTES)) ||
+        ((reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(w_down) | reinterpret_cast<uintptr_t>(rx) |
+          reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(xbuf) |
+          reinterpret_cast<uintptr_t>(w_o) | reinterpret_cast<uintptr_t>(o_x)) & 15) ||
+        (reinterpret_cast<uintptr_t>(qkv_x) & 3) || (reinterpret_cast<uintptr_t>(resid) & 1))
+        return (int)hipErrorInvalidValue;
+    const int N = (Hq + 2 * Hkv) * D;
+    QkvGemvArgs g{nullptr, K, nullptr, norm_w, eps, nullptr, w, N, qkv_x};
+    g.xw = rx;
+    g.n_done = n_down;
+    g.err = err;
+    DecodeArgs a{nullptr, N, nullptr, 0, q_norm_w, k_norm_w, cos_table, sin_table, pos, cache_k, cache_v,
+                 nullptr, nullptr, nullptr, Hq, Hkv, capacity, splits, eps, scale, 1, qkv_x, err, o_x};
+    OprojArgs o{w_o, K, resid, nullptr, nullptr, o_x, next_w, next_rows, next_group, nullptr};
+    o.rx = rx;
+    const DownArgs dn{w_down, act, resid, rx, K};
+    return qkv_attn_launch(X_WORDS, g, a, o, dn, kud, n_down, xbuf, layer, K, grid, stream);
 }
 
 extern "C" int q3_attn_merge(const float* part_acc, const float* part_ml, bf16_t* out, int B, int Hq,

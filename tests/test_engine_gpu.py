@@ -242,6 +242,32 @@ def test_qkv_attention_launch_matches_separate_projection(tile_engine, tile_ckpt
     assert runs[True][0] == runs[False][0] == runs[True][2] == runs[True][3] == runs[False][2]
 
 
+@pytest.mark.parametrize("prompt", [300, 900])
+def test_down_projection_in_attention_launch(tile_engine, tile_ckpt, prompt):
+    """At one row the down projection and its residual join run at the start
+    of the next layer's fused launch (q3_down_qkv_attn): the same bits as the
+    down projection launched on its own, at every step of trace_logits and
+    generate, across repeated calls."""
+    saved = engine_mod.DOWN_ATTENTION
+    cfg, _ = load_checkpoint(tile_ckpt)
+    rng = np.random.Generator(np.random.PCG64(970 + prompt))
+    ids = rng.integers(0, cfg.vocab_size, (1, prompt)).tolist()
+    runs = {}
+    try:
+        for joined in (True, False):
+            engine_mod.DOWN_ATTENTION = joined
+            steps, logits = tile_engine.trace_logits(ids, 8)
+            assert tile_engine.down_attn == joined and tile_engine.qkv_attn_o
+            tokens = list(tile_engine.generate(ids, 8))
+            again = list(tile_engine.generate(ids, 8))
+            assert int(tile_engine.attn_err.cpu()[0]) == 0
+            runs[joined] = (steps, logits, tokens, again)
+    finally:
+        engine_mod.DOWN_ATTENTION = saved
+    assert torch.equal(runs[True][1], runs[False][1])
+    assert runs[True][0] == runs[False][0] == runs[True][2] == runs[True][3] == runs[False][2]
+
+
 def test_batch_rows_are_independent(tiny_engine):
     """A row's tokens do not depend on the other rows of the batch (bit-identical)."""
     rng = np.random.Generator(np.random.PCG64(3))

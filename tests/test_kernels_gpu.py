@@ -1027,6 +1027,100 @@ def test_qkv_attn_matches_projection_then_fused_attention(B, Hkv, K, C, pos, spl
     assert err.item() == 0
 
 
+@pytest.mark.parametrize("Hkv,K,I,C,pos,splits", [
+    (8, 2560, 9728, 1536, 1100, 16),  # config 2's shape
+    (8, 2560, 9728, 1536, 1535, 16),  # last slot
+    (8, 2560, 9728, 64, 0, 2),        # config 1's grid (224: 11-12 down rows a workgroup), first position
+    (2, 512, 1024, 300, 200, 3)])     # the tile test model's widths
+def test_down_qkv_attn_matches_down_then_qkv_attn(Hkv, K, I, C, pos, splits):
+    """q3_down_qkv_attn == q3_gemv (X_PLAIN, EPI_RESID: the previous layer's
+    down projection and residual join) then q3_qkv_attn (X_NORM, with the o
+    projection), bit for bit: the residual after the o join, both caches and
+    the q|k|v and attention-output words; the down words rx hold the joined
+    residual with this step's flag.  Over several layers' flags, and again
+    after the exchange words are zeroed at a repeated (position, layer)."""
+    Hq, D, B = 4 * Hkv, 128, 1
+    N, KO = (Hq + 2 * Hkv) * D, Hq * D
+    assert call("q3_down_qkv_attn_grid", Hq, Hkv, C, splits, K, I) > 0
+    n_down = call("q3_down_qkv_attn_grid", Hq, Hkv, C, splits, K, I)  # every workgroup has down rows
+    qw = dv((1 + rnd((D,), 0.2, 2).float()).to(torch.bfloat16))
+    kw = dv((1 + rnd((D,), 0.2, 3).float()).to(torch.bfloat16))
+    cos, sin = oc.rope_tables(5e6, D, max(4096, C + 1))
+    cos, sin = dv(cos), dv(sin)
+    ck, cv = rnd((B, Hkv, C, D), 1.0, 4), rnd((B, Hkv, C, D), 1.0, 5)
+    posd = dv(torch.tensor([pos]))
+    words = call("q3_attn_xbuf_words", B, Hq, splits)
+    xbufs = [torch.zeros(words, dtype=torch.int32, device=DEV) for _ in range(2)]
+    qxs = [torch.zeros(N, dtype=torch.int32, device=DEV) for _ in range(2)]
+    oxs = [torch.zeros(KO, dtype=torch.int32, device=DEV) for _ in range(2)]
+    rx = torch.zeros(call("q3_down_rx_words", K), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for layer, seed in ((1, 21), (2, 22), (1, 23)):
+        if seed == 23:  # the same (position, layer) as the first round
+            for t in xbufs + qxs + oxs + [rx]:
+                t.zero_()
+        resid0 = rnd((B, K), 1.5, seed)
+        act = dv(rnd((B, I), 0.5, seed + 1))
+        wd = dv(rnd((K, I), 0.02, seed + 2))
+        g = dv((1 + rnd((K,), 0.2, seed + 50).float()).to(torch.bfloat16))
+        w = dv(rnd((N, K), 0.05, seed + 100))
+        wo = dv(rnd((K, KO), 0.05, seed + 200))
+        runs = []
+        for joined in (False, True):
+            ckd, cvd = dv(ck), dv(cv)
+            resid = dv(resid0)
+            if not joined:
+                gemv(_lib.X_PLAIN, act, I, wd, B, K, I, _lib.EPI_RESID, resid, K)
+                torch.cuda.synchronize()
+                after_down = resid.cpu()
+                call("q3_qkv_attn", _lib.X_NORM, P(resid), K, None, P(g), 1e-6, P(resid), P(w), K, P(qxs[0]),
+                     P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd), P(cvd), P(xbufs[0]), None, P(wo), P(oxs[0]),
+                     P(w), N, 16, B, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
+            else:
+                call("q3_down_qkv_attn", P(act), P(wd), I, P(rx), P(resid), P(g), 1e-6, P(w), K, P(qxs[1]),
+                     P(qw), P(kw), P(cos), P(sin), P(posd), P(ckd), P(cvd), P(xbufs[1]), P(wo), P(oxs[1]), P(w),
+                     N, 16, Hq, Hkv, C, splits, layer, D ** -0.5, P(err), S())
+            torch.cuda.synchronize()
+            runs.append((resid.cpu(), ckd.cpu(), cvd.cpu()))
+        (r0, k0, v0), (r1, k1, v1) = runs
+        assert torch.equal(r1, r0) and torch.equal(k1, k0) and torch.equal(v1, v0), (layer, seed)
+        assert torch.equal(qxs[1], qxs[0]) and torch.equal(oxs[1], oxs[0]), (layer, seed)
+        flag = 1 + (pos * 64 + layer) % 65535
+        rxv = rx.cpu().numpy().view(np.uint32)
+        assert (rxv[:K + n_down] >> 16 == flag).all()
+        assert np.array_equal((rxv[:K] & 0xffff).astype(np.uint16), after_down.view(torch.int16).numpy()
+                              .view(np.uint16).reshape(-1))
+    assert err.item() == 0
+
+
+def test_down_qkv_attn_refuses_what_it_is_not_built_for():
+    """Other widths, and a layer past the flag's field, are refused before
+    anything is enqueued."""
+    assert call("q3_down_qkv_attn_grid", 32, 8, 1536, 16, 2560, 9728) == 256
+    assert call("q3_down_qkv_attn_grid", 32, 8, 64, 2, 2560, 9728) == 224   # 11-12 down rows a workgroup
+    assert call("q3_down_qkv_attn_grid", 32, 8, 1536, 16, 2560, 8192) == 0
+    assert call("q3_down_qkv_attn_grid", 32, 8, 1536, 1, 2560, 9728) == 0   # one split: no fused attention
+    assert call("q3_down_qkv_attn_grid", 32, 8, 1536, 16, 4096, 9728) == 0
+    Hq, Hkv, D, C, splits, K, I = 32, 8, 128, 1536, 16, 2560, 9728
+    N = (Hq + 2 * Hkv) * D
+    z = lambda *shape: torch.zeros(*shape, dtype=torch.bfloat16, device=DEV)  # noqa: E731
+    act, wd, resid, w, wo, gain = z(I), z(K, I), z(K), z(N, K), z(K, Hq * D), z(K)
+    cos, sin = dv(oc.rope_tables(5e6, D, C + 1)[0]), dv(oc.rope_tables(5e6, D, C + 1)[1])
+    ck, cv = z(1, Hkv, C, D), z(1, Hkv, C, D)
+    posd = dv(torch.tensor([5]))
+    xbuf = torch.zeros(call("q3_attn_xbuf_words", 1, Hq, splits), dtype=torch.int32, device=DEV)
+    qx = torch.zeros(N, dtype=torch.int32, device=DEV)
+    ox = torch.zeros(Hq * D, dtype=torch.int32, device=DEV)
+    rx = torch.zeros(call("q3_down_rx_words", K), dtype=torch.int32, device=DEV)
+    for layer, ii in ((64, I), (-1, I), (3, 8192)):
+        with pytest.raises(RuntimeError):
+            call("q3_down_qkv_attn", P(act), P(wd), ii, P(rx), P(resid), P(gain), 1e-6, P(w), K, P(qx), P(gain),
+                 P(gain), P(cos), P(sin), P(posd), P(ck), P(cv), P(xbuf), P(wo), P(ox), None, 0, 0, Hq, Hkv, C,
+                 splits, layer, D ** -0.5, None, S())
+    torch.cuda.synchronize()
+    assert int(rx.abs().sum()) == 0 and int(qx.abs().sum()) == 0 and int(ck.float().abs().sum()) == 0
+
+
 def test_qkv_attn_refuses_what_it_is_not_built_for():
     """Three rows, other widths, the o projection at two rows and layers past
     the flag's field are refused before anything is enqueued."""
