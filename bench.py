@@ -136,7 +136,9 @@ def kernel_rooflines(eng, wl) -> list[dict]:
     q|k|v projection, attention, split merge and o projection + residual join:
     the q|k|v and o weights, K+V of every cached key at the current position,
     the residual read and written, the gains and the appended key and value
-    (the gate/up rows it warms into L2 are not counted).  B = 5..64: decode attention at the
+    (the gate/up rows it warms into L2 are not counted); where that launch
+    also runs the previous layer's down projection (every layer but the
+    first), its weights and input row too, averaged over the layers.  B = 5..64: decode attention at the
     current position (K+V of every cached key of every (sequence, KV head),
     the q|k|v rows in, the output rows out, the appended key and value) and
     the MFMA gate/up projection (weight, input rows, activations out).
@@ -164,9 +166,15 @@ def kernel_rooflines(eng, wl) -> list[dict]:
             Hkv, Hq, D = eng.KV_HEADS, eng.HEADS, eng.HEAD_DIM
             fused = (eng.qkv_size * H * 2 + H * Hq * D * 2 + B * Hkv * ctx * D * 2 * 2 + 2 * B * H * 2
                      + (H + 2 * D) * 2 + B * Hkv * D * 2 * 2)
+            name = f"q|k|v GEMV + attention + {eng.splits}-split merge + o GEMV + residual"
+            if eng.down_attn:
+                # Layers 1..L-1 also stream the previous layer's down weights
+                # and its input row: the mean over the timed layers.
+                L_ = len(eng.layers)
+                fused += (L_ - 1) * (H * I * 2 + B * I * 2) // L_
+                name = f"down GEMV + residual (layers 1-{L_ - 1}) + " + name
             ms = time_layer_graph(eng, eng._qkv_attn_layer, clear_exchange=True)
-            out.append(kernel_line(f"qkv_attn (q|k|v GEMV + attention + {eng.splits}-split merge + o GEMV + "
-                                   f"residual, one launch, context {ctx})", fused, ms,
+            out.append(kernel_line(f"qkv_attn ({name}, one launch, context {ctx})", fused, ms,
                                    f"qkv_attn_{tag}_traffic.txt"))
     elif eng.skinny:
         T = lambda w: eng.tiled[id(w)].data_ptr()  # noqa: E731
