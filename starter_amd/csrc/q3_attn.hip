@@ -1491,7 +1491,9 @@ extern "C" int q3_attn_splits(int B, int Hkv, int capacity) {
     // that leaves CUs idle (short contexts at small batch), 96 keys per split
     // where that is at most 16 splits (the fused merge's width), else 128, to
     // spread the latency-bound work (B=1 at 1536 keys: a 1.836 ms step at 16
-    // splits of 96 keys, against 1.848 at 12 of 128 and 1.865 at 8 of 192).
+    // splits of 96 keys, against 1.848 at 12 of 128 and 1.865 at 8 of 192;
+    // with the down, q|k|v, attention and o rows in one launch 1.600 ms at 16,
+    // 1.604 at 12, 1.658 at 8).
     const long heads = (long)B * Hkv;
     if (heads >= 512 || (heads >= 128 && capacity <= 4096)) return 1;
     const long groups = heads >= 64 ? 768 : 512;
