@@ -1018,7 +1018,8 @@ __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32
 // gemv_dot2_kernel (X_PLAIN from LDS, EPI_RESID), so rx carries the bits
 // q3_gemv would store.  Workgroup dg takes rows dg + n_down j < H (j < rpw,
 // 8..12 of them), wave w those with j = w + 4 i: the first two rows' weights
-// are in flight before the input is staged, a third follows their sums.  A
+// are in flight before the input is staged, a third follows the first row's
+// sums.  A
 // CU streams its down rows before its q|k|v rows, which then wait for every
 // workgroup's down rows while their own weights stream.
 struct DownArgs {
@@ -1066,24 +1067,28 @@ __device__ __forceinline__ void down_unit(const DownArgs& d, int dg, int n_down,
     }
     __syncthreads();
 
-    // The first two rows in one pass (each input chunk read from LDS once).
+    // The first row's sums, then the third row's loads into its registers
+    // (in flight while the second row's sums run), then the other two.
+    // Nothing moves across the barriers: otherwise the third row's loads get
+    // registers of their own next to wa's and spill.
     float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
 #pragma unroll
-    for (int u = 0; u < KUD; ++u) {
-        const u32x4_t xc = *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512);
-        acc0 = dot8v(wa[u], xc, acc0);
-        acc1 = dot8v(wb[u], xc, acc1);
-    }
-    // Their sums first, and nothing moved across: otherwise the third row's
-    // loads get registers of their own next to wa's and spill.
+    for (int u = 0; u < KUD; ++u)
+        acc0 = dot8v(wa[u], *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512), acc0);
     acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
     __builtin_amdgcn_sched_barrier(0);
     if (nr == 3) {
 #pragma unroll
         for (int u = 0; u < KUD; ++u)
             wa[u] = __builtin_nontemporal_load(
                 reinterpret_cast<const u32x4_t*>(d.w + (int64_t)r2 * K + lane * 8 + u * 512));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < KUD; ++u)
+        acc1 = dot8v(wb[u], *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512), acc1);
+    acc1 = wave_sum(acc1);
+    if (nr == 3) {
 #pragma unroll
         for (int u = 0; u < KUD; ++u)
             acc2 = dot8v(wa[u], *reinterpret_cast<const u32x4_t*>(xs + lane * 8 + u * 512), acc2);
