@@ -1019,9 +1019,8 @@ __device__ __forceinline__ void o_finish(const OprojArgs& o, int row0, const u32
 // q3_gemv would store.  Workgroup dg takes rows dg + n_down j < H (j < rpw,
 // 8..12 of them), wave w those with j = w + 4 i: the first two rows' weights
 // are in flight before the input is staged, a third follows the first row's
-// sums.  A
-// CU streams its down rows before its q|k|v rows, which then wait for every
-// workgroup's down rows while their own weights stream.
+// sums.  A CU streams its down rows before its q|k|v rows, which then wait
+// for every workgroup's down rows while their own weights stream.
 struct DownArgs {
     const bf16_t* w;      // W_down [H, 512 KUD]
     const bf16_t* act;    // its input row [512 KUD] (written by an earlier launch)
