@@ -1278,7 +1278,8 @@ constexpr long PREFILL_WIDE_WGS = 512;     // 32-query workgroups from this many
 // S^T = K.Q^T (16 MFMAs), the online softmax in base 2 (scores scaled by
 // scale*log2(e) inside one FMA; the causal mask only on blocks that cross the
 // diagonal of some query), P rounded to BF16 by v_cvt_pk_bf16_f32, and
-// O^T += V^T.P^T (16 MFMAs, V^T through transposing LDS reads).  Workgroups
+// O^T += V^T.P^T (16 MFMAs, V^T through transposing LDS reads) with two more
+// against a block of ones for the row sums.  Workgroups
 // start with the last queries (the longest causal ranges), so the short ones
 // fill the tail of the launch.
 template <int CB>
@@ -1344,15 +1345,19 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     };
 
     const float c = scale * 1.4426950408889634f;  // scores in base-2 units
-    float m[CB], l[CB];
-    f32x4_t acc[CB][8];
+    // acc[cb][8] accumulates P^T against a block of ones in place of V^T:
+    // every row of it is the running sum l of this column's probabilities
+    // (the BF16 values the other blocks multiply), rescaled with them, so the
+    // softmax takes no per-element adds or cross-lane sums for it.
+    float m[CB];
+    f32x4_t acc[CB][9];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
         m[cb] = -INFINITY;
-        l[cb] = 0.f;
 #pragma unroll
-        for (int dm = 0; dm < 8; ++dm) acc[cb][dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int dm = 0; dm < 9; ++dm) acc[cb][dm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+
 
     // One 64-key block from LDS stage st: S^T, online softmax, O^T += V^T.P^T.
     // MASK: some key of the block lies past some query (blocks that cross the
@@ -1398,21 +1403,15 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
             const float m_new = fmaxf(m[cb], group_max(mx));  // key 0 is visible to every query: finite
             const float alpha = __builtin_amdgcn_exp2f((m[cb] - m_new) * c);
             const float mc = m_new * c;
-            float sum = 0.f;
 #pragma unroll
             for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[cb][hb][i], c, -mc));
-                    s[cb][hb][i] = p;
-                    sum += p;
-                }
-            l[cb] = l[cb] * alpha + group_sum(sum);
+                for (int i = 0; i < 4; ++i) s[cb][hb][i] = __builtin_amdgcn_exp2f(fmaf(s[cb][hb][i], c, -mc));
             // The running maximum rarely grows once many keys are in: the rescale
             // is skipped when it grew for no query of the wave (alpha == 1).
             if (__any(m_new != m[cb])) {
 #pragma unroll
-                for (int dm = 0; dm < 8; ++dm) acc[cb][dm] *= alpha;
+                for (int dm = 0; dm < 9; ++dm) acc[cb][dm] *= alpha;
             }
             m[cb] = m_new;
             // P^T operand of k step j: keys 32j + 4g + t (t < 4), then 32j + 16 + 4g + t.
@@ -1433,8 +1432,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int dm = 0; dm < 8; ++dm) {
-                const bf16x8_t va = vt_operand_tr<true>(vt + j * 32 * D, dm, lane);
+            for (int dd = 0; dd < 9; ++dd) {
+                const int dm = (dd + 8) % 9;  // the ones block first
+                const bf16x8_t va = dm < 8 ? vt_operand_tr<true>(vt + j * 32 * D, dm, lane)
+                                           : as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
                     acc[cb][dm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][j], acc[cb][dm], 0, 0, 0);
@@ -1460,7 +1461,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     for (int cb = 0; cb < CB; ++cb) {
         const int qi = qb0 + 16 * cb + n;
         if (qi < T) {
-            const float inv_l = 1.0f / l[cb];
+            const float inv_l = 1.0f / acc[cb][8][0];
             bf16_t* dst = out + (((int64_t)b * T + qi) * Hq + h) * D;
 #pragma unroll
             for (int dm = 0; dm < 8; ++dm) {
