@@ -1446,15 +1446,19 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     const int n_full = min(nblk, full_end / PBLK);
     issue(0, 0);
     issue(1, min(1, nblk - 1) * PBLK);
-    for (int blk = 0; blk < nblk; ++blk) {
+    auto step = [&](auto mask, int blk) {
         const int st = blk & 1;
         q3dma::wait_vmcnt<2 * PDMA>();  // this block landed; the next one may be in flight
         __syncthreads();
-        if (blk < n_full) block(std::false_type{}, blk * PBLK, st);
-        else block(std::true_type{}, blk * PBLK, st);
+        block(mask, blk * PBLK, st);
         __syncthreads();  // every wave is done with this stage: refill it two blocks ahead
         issue(st, min(blk + 2, nblk - 1) * PBLK);
-    }
+    };
+    // Two loops rather than one with a per-block choice: a join of the two
+    // paths in one loop makes the compiler copy the accumulators every block.
+    int blk = 0;
+    for (; blk < n_full; ++blk) step(std::false_type{}, blk);
+    for (; blk < nblk; ++blk) step(std::true_type{}, blk);
     q3dma::wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
 #pragma unroll
