@@ -1471,7 +1471,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
             for (int dm = 0; dm < 8; ++dm) {
                 const f32x4_t& a = acc[cb][dm];
                 *reinterpret_cast<uint2*>(dst + 16 * dm + 4 * g) =
-                    make_uint2(pack2(f2bf(a[0] * inv_l), f2bf(a[1] * inv_l)), pack2(f2bf(a[2] * inv_l), f2bf(a[3] * inv_l)));
+                    make_uint2(pack_bf16x2(a[0] * inv_l, a[1] * inv_l), pack_bf16x2(a[2] * inv_l, a[3] * inv_l));
             }
         }
     }

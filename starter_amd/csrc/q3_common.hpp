@@ -36,6 +36,15 @@ __device__ __forceinline__ float rbf(float f) { return __uint_as_float(f2bf(f) <
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
+// pack2(f2bf(lo), f2bf(hi)) as one v_cvt_pk_bf16_f32 (round to nearest even,
+// the same bits for finite inputs).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
+}
+
 // --------------------------------------------------------------- reductions
 
 // Sum over the 64 lanes, returned to every lane.  DPP sums each 16-lane row

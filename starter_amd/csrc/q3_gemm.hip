@@ -59,18 +59,18 @@ __device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, cons
 template <int EPI>
 __device__ __forceinline__ void store4(bf16_t* y, int ldy, int m, int col, const f32x4_t& v) {
     if constexpr (EPI == Q3_EPI_SWIGLU) {
-        const uint32_t lo = f2bf(silu_bf16(rbf(v[0])) * rbf(v[1]));
-        const uint32_t hi = f2bf(silu_bf16(rbf(v[2])) * rbf(v[3]));
-        *reinterpret_cast<uint32_t*>(y + (int64_t)m * ldy + (col >> 1)) = pack2(lo, hi);
+        const uint32_t a = pack_bf16x2(v[0], v[1]), b = pack_bf16x2(v[2], v[3]);  // gate, up rounded
+        *reinterpret_cast<uint32_t*>(y + (int64_t)m * ldy + (col >> 1)) =
+            pack_bf16x2(silu_bf16(bflo(a)) * bfhi(a), silu_bf16(bflo(b)) * bfhi(b));
     } else {
         uint2* p = reinterpret_cast<uint2*>(y + (int64_t)m * ldy + col);
         if constexpr (EPI == Q3_EPI_RESID) {
             const uint2 r = *p;
-            const uint32_t e0 = f2bf(bflo(r.x) + rbf(v[0])), e1 = f2bf(bfhi(r.x) + rbf(v[1]));
-            const uint32_t e2 = f2bf(bflo(r.y) + rbf(v[2])), e3 = f2bf(bfhi(r.y) + rbf(v[3]));
-            *p = make_uint2(pack2(e0, e1), pack2(e2, e3));
+            const uint32_t a = pack_bf16x2(v[0], v[1]), b = pack_bf16x2(v[2], v[3]);
+            *p = make_uint2(pack_bf16x2(bflo(r.x) + bflo(a), bfhi(r.x) + bfhi(a)),
+                            pack_bf16x2(bflo(r.y) + bflo(b), bfhi(r.y) + bfhi(b)));
         } else {
-            *p = make_uint2(pack2(f2bf(v[0]), f2bf(v[1])), pack2(f2bf(v[2]), f2bf(v[3])));
+            *p = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
     }
 }
@@ -100,9 +100,10 @@ __device__ __forceinline__ void store_row16(const f32x4_t (&blk)[4], bf16_t* y, 
     if constexpr (EPI == Q3_EPI_SWIGLU) {
         uint32_t d[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            d[i] = pack2(f2bf(silu_bf16(rbf(blk[i][0])) * rbf(blk[i][1])),
-                         f2bf(silu_bf16(rbf(blk[i][2])) * rbf(blk[i][3])));
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = pack_bf16x2(blk[i][0], blk[i][1]), b = pack_bf16x2(blk[i][2], blk[i][3]);
+            d[i] = pack_bf16x2(silu_bf16(bflo(a)) * bfhi(a), silu_bf16(bflo(b)) * bfhi(b));
+        }
         const auto p01 = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
         const auto p23 = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
         const auto lo = __builtin_amdgcn_permlane32_swap(p01[0], p23[0], false, false);
@@ -115,10 +116,10 @@ __device__ __forceinline__ void store_row16(const f32x4_t (&blk)[4], bf16_t* y, 
         for (int i = 0; i < 4; i += 2) {
             const f32x4_t& p = blk[i];
             const f32x4_t& q = blk[i + 1];
-            const auto s0 = __builtin_amdgcn_permlane16_swap(pack2(f2bf(p[0]), f2bf(p[1])),
-                                                             pack2(f2bf(q[0]), f2bf(q[1])), false, false);
-            const auto s1 = __builtin_amdgcn_permlane16_swap(pack2(f2bf(p[2]), f2bf(p[3])),
-                                                             pack2(f2bf(q[2]), f2bf(q[3])), false, false);
+            const auto s0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(p[0], p[1]), pack_bf16x2(q[0], q[1]),
+                                                             false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(p[2], p[3]), pack_bf16x2(q[2], q[3]),
+                                                             false, false);
             const int col = c0 + 16 * (i + (g & 1)) + 8 * (g >> 1);
             if (row_ok && col < N) {
                 uint4* dst = reinterpret_cast<uint4*>(y + (int64_t)m * ldy + col);
@@ -126,7 +127,7 @@ __device__ __forceinline__ void store_row16(const f32x4_t (&blk)[4], bf16_t* y, 
                 if constexpr (EPI == Q3_EPI_RESID) {
                     const uint4 r = *dst;
                     auto join = [](uint32_t rw, uint32_t vw) {
-                        return pack2(f2bf(bflo(rw) + bflo(vw)), f2bf(bfhi(rw) + bfhi(vw)));
+                        return pack_bf16x2(bflo(rw) + bflo(vw), bfhi(rw) + bfhi(vw));
                     };
                     v = make_uint4(join(r.x, v.x), join(r.y, v.y), join(r.z, v.z), join(r.w, v.w));
                 }
