@@ -1445,14 +1445,15 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(const bf16_t* 
     // workgroup (keys <= start + qb0); the rest cross the diagonal.
     const int n_full = min(nblk, full_end / PBLK);
     issue(0, 0);
-    issue(1, min(1, nblk - 1) * PBLK);
     auto step = [&](auto mask, int blk) {
         const int st = blk & 1;
-        q3dma::wait_vmcnt<2 * PDMA>();  // this block landed; the next one may be in flight
+        q3dma::wait_vmcnt<0>();  // this block landed (the only loads in flight)
+        // One barrier per block: past it every wave sees this block, and every
+        // wave is done with the other stage (block blk - 1), which then takes
+        // the next block while this one computes.
         __syncthreads();
+        if (blk + 1 < nblk) issue(st ^ 1, (blk + 1) * PBLK);
         block(mask, blk * PBLK, st);
-        __syncthreads();  // every wave is done with this stage: refill it two blocks ahead
-        issue(st, min(blk + 2, nblk - 1) * PBLK);
     };
     // Two loops rather than one with a per-block choice: a join of the two
     // paths in one loop makes the compiler copy the accumulators every block.
